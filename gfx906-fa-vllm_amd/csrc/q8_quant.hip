@@ -1,0 +1,247 @@
+// q8_quant.hip - Q8_0 quantize and paged cache-write kernels for gfx950.
+//
+// Work mapping: a Q8_0 block of 32 values lives on one 16-lane DPP row, two
+// values per lane, so one wave64 quantizes 4 blocks (one D=128 row) with the
+// amax reduction entirely in DPP (no LDS, no barriers).
+//
+//   q8_dense_kernel          rows [N, D] -> AoS rows          (reference:
+//                            extension/gfx906_fa_quant.cu:100-129)
+//   q8_reshape_cache_kernel  key rows -> AoS paged cache     (reference:
+//                            extension/gfx906_fa_quant.cu:150-200)
+//   q8_cache_write_kv_kernel key AND value rows -> planar paged cache (the
+//                            backend's hot-path write; no reference kernel
+//                            writes V, extension/gfx906_fa.cpp:322-326)
+#include <cstdio>
+
+#include "q8_common.h"
+
+using namespace gfa;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Dense: blocks are consecutive (row-major [N, D] with D % 32 == 0), so the
+// input is a flat array of nblk = N*D/32 blocks and the output a flat array of
+// nblk 34-byte blocks.  One 16-lane row per block, lane owns values 2i, 2i+1.
+template <int DT>
+__global__ __launch_bounds__(256) void q8_dense_kernel(const void *__restrict__ x,
+                                                      uint8_t *__restrict__ y, int64_t nblk) {
+    const int lane16 = threadIdx.x & 15;
+    const int64_t blk = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    // every lane of a 16-lane row shares blk, so rows retire together (the
+    // DPP reduction only mixes lanes of the same row).
+    if (blk >= nblk) return;
+    float a, b;
+    load2_as_f32<DT>(x, blk * QK + 2 * lane16, a, b);
+    const Q8Pair r = q8_quantize_pair(a, b);
+    uint8_t *o = y + blk * QBYTES;
+    // 34*blk + 2 + 2*lane16 is even: 16-bit stores are aligned.
+    *reinterpret_cast<uint16_t *>(o + 2 + 2 * lane16) =
+        (uint16_t)((uint8_t)r.qa | ((uint16_t)(uint8_t)r.qb << 8));
+    if (lane16 == 0) *reinterpret_cast<uint16_t *>(o) = f32_to_half_bits(r.d);
+}
+
+// ---------------------------------------------------------------------------
+// AoS paged write with arbitrary strides (reference contract).  One wave per
+// (token, kv-head); each of the 4 DPP rows takes one block per iteration.
+// Stores are bytewise so any byte stride works.
+template <int DT>
+__global__ __launch_bounds__(256) void q8_reshape_cache_kernel(
+    const void *__restrict__ key, const int64_t *__restrict__ slot_mapping,
+    uint8_t *__restrict__ cache, int num_tokens, int num_kv_heads, int head_size,
+    int block_size, int64_t kts, int64_t khs, int64_t cbs, int64_t cts, int64_t chs) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= num_tokens * num_kv_heads) return;
+    const int t = wave / num_kv_heads;
+    const int h = wave - t * num_kv_heads;
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) return;
+    const int64_t blk = slot / block_size;
+    const int64_t off = slot - blk * block_size;
+    const int64_t xb = (int64_t)t * kts + (int64_t)h * khs;
+    uint8_t *row = cache + blk * cbs + off * cts + (int64_t)h * chs;
+    const int nb = head_size / QK;
+    const int lane16 = lane & 15;
+    for (int b0 = 0; b0 < nb; b0 += 4) {
+        const int b = b0 + (lane >> 4);
+        if (b < nb) {  // uniform across the 16-lane row
+            const float a = load_as_f32<DT>(key, xb + b * QK + 2 * lane16);
+            const float c = load_as_f32<DT>(key, xb + b * QK + 2 * lane16 + 1);
+            const Q8Pair r = q8_quantize_pair(a, c);
+            uint8_t *o = row + b * QBYTES;
+            o[2 + 2 * lane16] = (uint8_t)r.qa;
+            o[3 + 2 * lane16] = (uint8_t)r.qb;
+            if (lane16 == 0) {
+                const uint16_t hb = f32_to_half_bits(r.d);
+                o[0] = (uint8_t)(hb & 0xFF);
+                o[1] = (uint8_t)(hb >> 8);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Planar K+V write (D = 128).  One wave per (token, kv-head): lane l holds
+// dims 2l, 2l+1 of K and of V; block b = l/16 is the lane's DPP row.
+//   K ints : u16 store at t*128 + kpos(2l)   (2l, 2l+1 share an 8-group)
+//   V ints : two byte stores at vpos(t, 2l), vpos(t, 2l+1)
+//   scales : lane 16b writes fp16 scale[t][b] of K and of V
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
+    const void *__restrict__ key, const void *__restrict__ value,
+    const int64_t *__restrict__ slot_mapping, uint8_t *__restrict__ kc,
+    uint8_t *__restrict__ vc, int num_tokens, int num_kv_heads, int block_size,
+    int64_t kts, int64_t khs, int64_t vts, int64_t vhs, int64_t cbs, int64_t chs) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= num_tokens * num_kv_heads) return;
+    const int t = wave / num_kv_heads;
+    const int h = wave - t * num_kv_heads;
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) return;
+    const int64_t page = slot / block_size;
+    const int off = (int)(slot - page * block_size);
+    const int sp = off >> 4, tt = off & 15;
+    const int64_t base = page * cbs + (int64_t)h * chs + (int64_t)sp * SUBPAGE_BYTES;
+
+    const int d0 = 2 * lane;
+    float ka, kb, va, vb;
+    if constexpr (VEC) {
+        load2_as_f32<DT>(key, (int64_t)t * kts + (int64_t)h * khs + d0, ka, kb);
+        load2_as_f32<DT>(value, (int64_t)t * vts + (int64_t)h * vhs + d0, va, vb);
+    } else {
+        ka = load_as_f32<DT>(key, (int64_t)t * kts + (int64_t)h * khs + d0);
+        kb = load_as_f32<DT>(key, (int64_t)t * kts + (int64_t)h * khs + d0 + 1);
+        va = load_as_f32<DT>(value, (int64_t)t * vts + (int64_t)h * vhs + d0);
+        vb = load_as_f32<DT>(value, (int64_t)t * vts + (int64_t)h * vhs + d0 + 1);
+    }
+    const Q8Pair rk = q8_quantize_pair(ka, kb);
+    const Q8Pair rv = q8_quantize_pair(va, vb);
+
+    const int b = lane >> 4;
+    // K: kpos(d) = 32*((d%32)/8) + 8*(d/32) + d%8
+    const int kpos = 32 * ((d0 & 31) >> 3) + 8 * (d0 >> 5) + (d0 & 7);
+    *reinterpret_cast<uint16_t *>(kc + base + tt * 128 + kpos) =
+        (uint16_t)((uint8_t)rk.qa | ((uint16_t)(uint8_t)rk.qb << 8));
+    // V: vpos(t, d) = ((t/4)*16 + d%16)*32 + (d/16)*4 + t%4
+    const int vrow = ((tt >> 2) * 16) * 32 + (d0 >> 4) * 4 + (tt & 3);
+    vc[base + vrow + (d0 & 15) * 32] = (uint8_t)rv.qa;
+    vc[base + vrow + ((d0 + 1) & 15) * 32] = (uint8_t)rv.qb;
+    if ((lane & 15) == 0) {
+        const int so = SCALE_OFF + (4 * tt + b) * 2;
+        *reinterpret_cast<uint16_t *>(kc + base + so) = f32_to_half_bits(rk.d);
+        *reinterpret_cast<uint16_t *>(vc + base + so) = f32_to_half_bits(rv.d);
+    }
+}
+
+bool bad_dtype(int dt) { return dt != GFA_DTYPE_F32 && dt != GFA_DTYPE_F16 && dt != GFA_DTYPE_BF16; }
+
+}  // namespace
+
+extern "C" const char *gfx906_fa_amd_version(void) { return "gfx906_fa_amd 0.1 gfx950"; }
+
+extern "C" hipError_t gfx906_fa_amd_quantize_q8_0(const void *x, int x_dtype, uint8_t *y,
+                                                  int64_t N, int D, hipStream_t stream) {
+    if (D <= 0 || D % QK != 0 || N < 0 || bad_dtype(x_dtype)) {
+        fprintf(stderr, "[gfx906_fa_amd] quantize_q8_0: need D %% 32 == 0 (D=%d), N >= 0, dtype 0/1/2\n", D);
+        return hipErrorInvalidValue;
+    }
+    if (N == 0) return hipSuccess;
+    const int64_t nblk = N * (D / QK);
+    const int64_t threads = nblk * 16;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    switch (x_dtype) {
+        case GFA_DTYPE_F32: q8_dense_kernel<GFA_DTYPE_F32><<<grid, 256, 0, stream>>>(x, y, nblk); break;
+        case GFA_DTYPE_F16: q8_dense_kernel<GFA_DTYPE_F16><<<grid, 256, 0, stream>>>(x, y, nblk); break;
+        default: q8_dense_kernel<GFA_DTYPE_BF16><<<grid, 256, 0, stream>>>(x, y, nblk); break;
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t launch_quantize_q8_0_dense(const void *x, uint8_t *y, int N, int D,
+                                                 hipStream_t stream) {
+    return gfx906_fa_amd_quantize_q8_0(x, GFA_DTYPE_F16, y, N, D, stream);
+}
+
+extern "C" hipError_t gfx906_fa_amd_reshape_and_cache_q8(
+    const void *key, int key_dtype, const int64_t *slot_mapping, uint8_t *k_cache_q8,
+    int num_tokens, int num_kv_heads, int head_size, int block_size, int64_t kts, int64_t khs,
+    int64_t cbs, int64_t cts, int64_t chs, hipStream_t stream) {
+    if (head_size <= 0 || head_size % QK != 0 || block_size <= 0 || bad_dtype(key_dtype) ||
+        num_kv_heads <= 0 || num_tokens < 0) {
+        fprintf(stderr, "[gfx906_fa_amd] reshape_and_cache_q8: bad arguments (head_size=%d, block_size=%d)\n",
+                head_size, block_size);
+        return hipErrorInvalidValue;
+    }
+    if (num_tokens == 0) return hipSuccess;
+    const int64_t waves = (int64_t)num_tokens * num_kv_heads;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+#define GFA_LAUNCH_RC(DT)                                                                   \
+    q8_reshape_cache_kernel<DT><<<grid, 256, 0, stream>>>(key, slot_mapping, k_cache_q8,   \
+                                                         num_tokens, num_kv_heads,          \
+                                                         head_size, block_size, kts, khs,   \
+                                                         cbs, cts, chs)
+    switch (key_dtype) {
+        case GFA_DTYPE_F32: GFA_LAUNCH_RC(GFA_DTYPE_F32); break;
+        case GFA_DTYPE_F16: GFA_LAUNCH_RC(GFA_DTYPE_F16); break;
+        default: GFA_LAUNCH_RC(GFA_DTYPE_BF16); break;
+    }
+#undef GFA_LAUNCH_RC
+    return hipGetLastError();
+}
+
+extern "C" hipError_t launch_reshape_and_cache_q8(const void *key, const int64_t *slot_mapping,
+                                                  uint8_t *k_cache_q8, int num_tokens,
+                                                  int num_kv_heads, int head_size,
+                                                  int block_size, int64_t kts, int64_t khs,
+                                                  int64_t cbs, int64_t cts, int64_t chs,
+                                                  hipStream_t stream) {
+    return gfx906_fa_amd_reshape_and_cache_q8(key, GFA_DTYPE_F16, slot_mapping, k_cache_q8,
+                                              num_tokens, num_kv_heads, head_size, block_size,
+                                              kts, khs, cbs, cts, chs, stream);
+}
+
+extern "C" hipError_t gfx906_fa_amd_cache_write_kv(
+    const void *key, const void *value, int dtype, const int64_t *slot_mapping, uint8_t *k_cache,
+    uint8_t *v_cache, int num_tokens, int num_kv_heads, int head_size, int block_size,
+    int64_t kts, int64_t khs, int64_t vts, int64_t vhs, int64_t cbs, int64_t chs,
+    hipStream_t stream) {
+    if (head_size != 128 || block_size <= 0 || block_size % SUBPAGE != 0 || bad_dtype(dtype) ||
+        num_kv_heads <= 0 || num_tokens < 0) {
+        fprintf(stderr,
+                "[gfx906_fa_amd] cache_write_kv: need head_size == 128 (got %d) and block_size %% 16 == 0 (got %d)\n",
+                head_size, block_size);
+        return hipErrorInvalidValue;
+    }
+    if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uint64_t)cbs | (uint64_t)chs) & 1u) {
+        fprintf(stderr, "[gfx906_fa_amd] cache_write_kv: cache bases and strides must be even\n");
+        return hipErrorInvalidValue;
+    }
+    if (num_tokens == 0) return hipSuccess;
+    const int esz = dtype == GFA_DTYPE_F32 ? 4 : 2;
+    const bool vec = (((uintptr_t)key | (uintptr_t)value) % (2 * esz) == 0) && (kts % 2 == 0) &&
+                     (khs % 2 == 0) && (vts % 2 == 0) && (vhs % 2 == 0);
+    const int64_t waves = (int64_t)num_tokens * num_kv_heads;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+#define GFA_LAUNCH_KV(DT, V)                                                                 \
+    q8_cache_write_kv_kernel<DT, V><<<grid, 256, 0, stream>>>(key, value, slot_mapping,     \
+                                                             k_cache, v_cache, num_tokens,   \
+                                                             num_kv_heads, block_size, kts,  \
+                                                             khs, vts, vhs, cbs, chs)
+    if (vec) {
+        switch (dtype) {
+            case GFA_DTYPE_F32: GFA_LAUNCH_KV(GFA_DTYPE_F32, true); break;
+            case GFA_DTYPE_F16: GFA_LAUNCH_KV(GFA_DTYPE_F16, true); break;
+            default: GFA_LAUNCH_KV(GFA_DTYPE_BF16, true); break;
+        }
+    } else {
+        switch (dtype) {
+            case GFA_DTYPE_F32: GFA_LAUNCH_KV(GFA_DTYPE_F32, false); break;
+            case GFA_DTYPE_F16: GFA_LAUNCH_KV(GFA_DTYPE_F16, false); break;
+            default: GFA_LAUNCH_KV(GFA_DTYPE_BF16, false); break;
+        }
+    }
+#undef GFA_LAUNCH_KV
+    return hipGetLastError();
+}

@@ -1,0 +1,394 @@
+"""``gfx906_fa`` op module for MI355X (gfx950).
+
+Mirrors the reference's pybind11 module (``extension/gfx906_fa.cpp:660-690``):
+same op names, argument names, defaults and error behaviour (a failed check
+raises ``RuntimeError``, as ``TORCH_CHECK`` does).  Each op validates its
+tensors, then calls one ``extern "C"`` entry point of ``libgfx906_fa_amd.so``
+(declared in ``include/gfx906_fa_amd.h``) on the current HIP stream.  There
+is no CPU fallback: importing this module without the built library, or
+calling an op on a CPU tensor, raises.
+
+Ops
+---
+quantize_q8_0(k_fp16)                                  extension/gfx906_fa.cpp:273-309
+reshape_and_cache_q8(key, slot_mapping, k_cache_q8)    extension/gfx906_fa.cpp:322-374
+gather_paged_kv_q8(key_cache_q8, value_cache, block_table, seq_lens, Sk,
+                   k_out=None, v_out=None)             extension/gfx906_fa.cpp:393-498
+forward_paged_direct(q, key_cache_q8, value_cache, block_table, seq_lens,
+                     scale, mask=None, q_abs_offset=None)
+                                                       extension/gfx906_fa.cpp:516-658
+New for the Q8 K+V cache of this backend:
+reshape_and_cache_q8_kv(key, value, slot_mapping, key_cache, value_cache)
+gather_paged_kv_q8q8(key_cache, value_cache, block_table, seq_lens, Sk, ...)
+paged_attention(query, key_cache, value_cache, block_table, seq_lens,
+                query_start_loc, max_query_len, max_seq_len, scale, out=None, ...)
+new_kv_cache(num_blocks, block_size, num_kv_heads, head_size=128, device=...)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgfx906_fa_amd.so")
+
+QK8_0 = 32
+Q8_0_BYTES = 34
+SUBPAGE_TOKENS = 16
+SUBPAGE_BYTES = 2176
+
+_DT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"gfx906_fa: HIP library not built ({LIB_PATH}); run "
+            "`python gfx906-fa-vllm_amd/build.py` (or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, I64, F, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+    sig = {
+        "gfx906_fa_amd_version": (ctypes.c_char_p, []),
+        "launch_quantize_q8_0_dense": (I, [P, P, I, I, P]),
+        "gfx906_fa_amd_quantize_q8_0": (I, [P, I, P, I64, I, P]),
+        "launch_reshape_and_cache_q8": (I, [P, P, P, I, I, I, I, I64, I64, I64, I64, I64, P]),
+        "gfx906_fa_amd_reshape_and_cache_q8": (I, [P, I, P, P, I, I, I, I, I64, I64, I64, I64, I64, P]),
+        "launch_gather_paged_kv_q8": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I,
+                                          I64, I64, I64, I64, I64, I64, P]),
+        "gfx906_fa_amd_gather_rows": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I,
+                                          I64, I64, I64, I64, I64, I64, P]),
+        "gfx906_fa_amd_gather_planar": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I64, I64, P]),
+        "gfx906_fa_amd_cache_write_kv": (I, [P, P, I, P, P, P, I, I, I, I,
+                                             I64, I64, I64, I64, I64, I64, P]),
+        "gfx906_fa_amd_paged_attention_workspace_size": (SZ, [I, I, I, I, I, I, I]),
+        "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
+                                              I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def lib():
+    return _load()
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _cuda(t: torch.Tensor, name: str) -> None:
+    _check(t.is_cuda, f"{name} must be CUDA/HIP")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _ok(err: int, what: str) -> None:
+    if err != 0:
+        raise RuntimeError(f"{what} failed: hipError {err}")
+
+
+# ---------------------------------------------------------------------------
+# Reference ops
+# ---------------------------------------------------------------------------
+def quantize_q8_0(k_fp16: torch.Tensor) -> torch.Tensor:
+    """Dense Q8_0 quantize of the last dim (fp16; bf16 / fp32 also accepted).
+    ``extension/gfx906_fa.cpp:273-309``."""
+    _cuda(k_fp16, "k_fp16")
+    _check(k_fp16.is_contiguous(), "k_fp16 must be contiguous")
+    _check(k_fp16.dtype in _DT, "k_fp16 must be fp16 (or bf16 / fp32)")
+    _check(k_fp16.dim() >= 1, "k_fp16 must have at least 1 dim")
+    D = k_fp16.shape[-1]
+    _check(D % QK8_0 == 0, "last dim must be multiple of 32")
+    N = k_fp16.numel() // D if D else 0
+    out = torch.empty((*k_fp16.shape[:-1], D // QK8_0 * Q8_0_BYTES), dtype=torch.uint8,
+                      device=k_fp16.device)
+    err = _load().gfx906_fa_amd_quantize_q8_0(_ptr(k_fp16), _DT[k_fp16.dtype], _ptr(out), N, D,
+                                              _stream(k_fp16.device))
+    _ok(err, "gfx906_fa_amd_quantize_q8_0")
+    return out
+
+
+def reshape_and_cache_q8(key: torch.Tensor, slot_mapping: torch.Tensor,
+                         k_cache_q8: torch.Tensor) -> None:
+    """Quantize key [T, Hkv, D] and scatter AoS rows into
+    k_cache_q8 [NB, bs, Hkv, (D/32)*34] at slot_mapping (int64, < 0 skips).
+    Strides of both tensors are honoured.  ``extension/gfx906_fa.cpp:322-374``."""
+    for t, n in ((key, "key"), (slot_mapping, "slot_mapping"), (k_cache_q8, "k_cache_q8")):
+        _cuda(t, n)
+    _check(key.dtype in _DT, "key must be fp16 (or bf16 / fp32)")
+    _check(slot_mapping.dtype == torch.int64, "slot_mapping must be int64")
+    _check(k_cache_q8.dtype == torch.uint8, "k_cache_q8 must be uint8")
+    _check(key.dim() == 3, "key must be [num_tokens, Hkv, D]")
+    _check(k_cache_q8.dim() == 4, "k_cache_q8 must be [B, bs, Hkv, bytes]")
+    T, Hkv, D = key.shape
+    _check(D % QK8_0 == 0, "head_size must be multiple of 32")
+    bpr = D // QK8_0 * Q8_0_BYTES
+    _check(k_cache_q8.shape[2] == Hkv,
+           f"k_cache_q8 Hkv mismatch: got {k_cache_q8.shape[2]} vs key Hkv={Hkv}")
+    _check(k_cache_q8.shape[3] == bpr,
+           f"k_cache_q8 last dim mismatch: got {k_cache_q8.shape[3]} expected {bpr}")
+    _check(k_cache_q8.stride(3) == 1, "k_cache_q8 rows must be contiguous")
+    _check(key.stride(2) == 1, "key rows must be contiguous")
+    _check(slot_mapping.shape[0] == T, "slot_mapping length mismatch")
+    sm = slot_mapping.contiguous()
+    err = _load().gfx906_fa_amd_reshape_and_cache_q8(
+        _ptr(key), _DT[key.dtype], _ptr(sm), _ptr(k_cache_q8), T, Hkv, D, k_cache_q8.shape[1],
+        key.stride(0), key.stride(1), k_cache_q8.stride(0), k_cache_q8.stride(1),
+        k_cache_q8.stride(2), _stream(key.device))
+    _ok(err, "launch_reshape_and_cache_q8")
+
+
+def gather_paged_kv_q8(key_cache_q8: torch.Tensor, value_cache: torch.Tensor,
+                       block_table: torch.Tensor, seq_lens: torch.Tensor, Sk: int,
+                       k_out: Optional[torch.Tensor] = None,
+                       v_out: Optional[torch.Tensor] = None):
+    """Paged AoS K (Q8_0 rows) + paged V rows -> contiguous BHSD
+    [k_out, v_out].  V rows past seq_lens (or on a -1 page) are zeroed, K rows
+    there are left as they were.  value_cache may be fp16 [NB, bs, Hkv, D]
+    (the reference contract) or uint8 AoS Q8_0 rows [NB, bs, Hkv, (D/32)*34]
+    (the Q8/Q8 variant).  Caller buffers are used only on an exact
+    shape/dtype/contiguity match (``extension/gfx906_fa.cpp:449-469``).
+    ``extension/gfx906_fa.cpp:393-498``."""
+    for t, n in ((key_cache_q8, "key_cache_q8"), (value_cache, "value_cache"),
+                 (block_table, "block_table"), (seq_lens, "seq_lens")):
+        _cuda(t, n)
+    _check(key_cache_q8.dtype == torch.uint8, "key_cache_q8 must be uint8")
+    _check(value_cache.dtype in (torch.float16, torch.uint8), "value_cache must be fp16 (or uint8 Q8_0 rows)")
+    _check(seq_lens.dtype == torch.int32, "seq_lens must be int32")
+    _check(key_cache_q8.dim() == 4, "key_cache_q8 must be 4D")
+    _check(value_cache.dim() == 4, "value_cache must be 4D")
+    NB, bs, Hkv, bpr = key_cache_q8.shape
+    vq8 = value_cache.dtype == torch.uint8
+    D = (value_cache.shape[3] // Q8_0_BYTES * QK8_0) if vq8 else value_cache.shape[3]
+    _check(value_cache.shape[0] == NB, "value_cache blocks mismatch")
+    _check(value_cache.shape[1] == bs, "value_cache block_size mismatch")
+    _check(value_cache.shape[2] == Hkv, "value_cache Hkv mismatch")
+    _check(D % QK8_0 == 0, "D must be multiple of 32")
+    _check(bpr == D // QK8_0 * Q8_0_BYTES,
+           f"bytes_per_row must equal (D/32)*34, got {bpr} vs expected {D // QK8_0 * Q8_0_BYTES}")
+    _check(block_table.dtype == torch.int32, "block_table must be int32 (caller should .to(torch.int32))")
+    _check(block_table.is_contiguous(), "block_table must be contiguous")
+    _check(seq_lens.is_contiguous(), "seq_lens must be contiguous")
+    B, M = block_table.shape
+    _check(seq_lens.shape[0] == B, "seq_lens vs block_table batch mismatch")
+    _check(Sk > 0 and Sk % 32 == 0, f"Sk must be positive multiple of 32, got {Sk}")
+    _check(key_cache_q8.stride(3) == 1 and value_cache.stride(3) == 1, "cache rows must be contiguous")
+    vrow = value_cache.shape[3]
+
+    def use_or_alloc(buf, dtype, dim3):
+        if (buf is not None and buf.dim() == 4 and tuple(buf.shape) == (B, Hkv, Sk, dim3)
+                and buf.dtype == dtype and buf.device == key_cache_q8.device and buf.is_contiguous()):
+            return buf
+        return torch.empty((B, Hkv, Sk, dim3), dtype=dtype, device=key_cache_q8.device)
+
+    k_o = use_or_alloc(k_out, torch.uint8, bpr)
+    v_o = use_or_alloc(v_out, value_cache.dtype, vrow)
+    es = value_cache.element_size()
+    err = _load().gfx906_fa_amd_gather_rows(
+        _ptr(key_cache_q8), _ptr(value_cache), _ptr(block_table), _ptr(seq_lens), _ptr(k_o),
+        _ptr(v_o), B, Hkv, Sk, bpr, vrow * es, bs, M,
+        key_cache_q8.stride(0), key_cache_q8.stride(1), key_cache_q8.stride(2),
+        value_cache.stride(0) * es, value_cache.stride(1) * es, value_cache.stride(2) * es,
+        _stream(key_cache_q8.device))
+    _ok(err, "launch_gather_paged_kv_q8")
+    return [k_o, v_o]
+
+
+# ---------------------------------------------------------------------------
+# Planar Q8 K+V cache of this backend
+# ---------------------------------------------------------------------------
+def new_kv_cache(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int = 128,
+                 device=None) -> torch.Tensor:
+    """Zeroed planar cache uint8 [NB, 2, Hkv, block_size/16*2176]
+    (dim 1: 0 = K plane, 1 = V plane)."""
+    _check(head_size == 128, "the planar Q8 cache supports head_size 128")
+    _check(block_size % SUBPAGE_TOKENS == 0, "block_size must be a multiple of 16")
+    return torch.zeros((num_blocks, 2, num_kv_heads, block_size // SUBPAGE_TOKENS * SUBPAGE_BYTES),
+                       dtype=torch.uint8, device=device)
+
+
+def _plane_info(key_cache: torch.Tensor, value_cache: torch.Tensor):
+    """Validates a planar (K, V) plane pair [NB, Hkv, bs/16*2176] (uint8, any
+    block/head strides, contiguous pages) -> (block_size, Hkv, block stride,
+    head stride)."""
+    _check(key_cache.dtype == torch.uint8 and value_cache.dtype == torch.uint8,
+           "key_cache / value_cache must be uint8 planar Q8 planes")
+    _check(key_cache.dim() == 3 and value_cache.dim() == 3,
+           "key_cache / value_cache must be [num_blocks, Hkv, block_size/16*2176]")
+    _check(key_cache.shape == value_cache.shape, "key_cache / value_cache shape mismatch")
+    _check(key_cache.stride() == value_cache.stride(), "key_cache / value_cache stride mismatch")
+    NB, Hkv, nbytes = key_cache.shape
+    _check(nbytes % SUBPAGE_BYTES == 0, "page bytes must be a multiple of 2176")
+    _check(key_cache.stride(2) == 1, "pages must be contiguous")
+    return nbytes // SUBPAGE_BYTES * SUBPAGE_TOKENS, Hkv, key_cache.stride(0), key_cache.stride(1)
+
+
+def reshape_and_cache_q8_kv(key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor,
+                            key_cache: torch.Tensor, value_cache: torch.Tensor) -> None:
+    """Quantize key and value [T, Hkv, 128] to Q8_0 and write them at
+    slot_mapping into the planar planes (one launch; slot < 0 skips)."""
+    for t, n in ((key, "key"), (value, "value"), (slot_mapping, "slot_mapping"),
+                 (key_cache, "key_cache"), (value_cache, "value_cache")):
+        _cuda(t, n)
+    _check(key.dtype in _DT and value.dtype == key.dtype, "key/value must share dtype fp16/bf16/fp32")
+    _check(key.dim() == 3 and value.shape == key.shape, "key/value must be [num_tokens, Hkv, D]")
+    _check(slot_mapping.dtype == torch.int64, "slot_mapping must be int64")
+    T, Hkv, D = key.shape
+    _check(D == 128, "head_size must be 128")
+    _check(key.stride(2) == 1 and value.stride(2) == 1, "key/value rows must be contiguous")
+    _check(slot_mapping.shape[0] == T, "slot_mapping length mismatch")
+    bs, Hc, cbs, chs = _plane_info(key_cache, value_cache)
+    _check(Hc == Hkv, f"cache Hkv mismatch: got {Hc} vs key Hkv={Hkv}")
+    sm = slot_mapping.contiguous()
+    err = _load().gfx906_fa_amd_cache_write_kv(
+        _ptr(key), _ptr(value), _DT[key.dtype], _ptr(sm), _ptr(key_cache), _ptr(value_cache), T,
+        Hkv, D, bs, key.stride(0), key.stride(1), value.stride(0), value.stride(1), cbs, chs,
+        _stream(key.device))
+    _ok(err, "gfx906_fa_amd_cache_write_kv")
+
+
+def gather_paged_kv_q8q8(key_cache: torch.Tensor, value_cache: torch.Tensor,
+                         block_table: torch.Tensor, seq_lens: torch.Tensor, Sk: int,
+                         k_out: Optional[torch.Tensor] = None,
+                         v_out: Optional[torch.Tensor] = None):
+    """Planar Q8 K+V planes -> contiguous AoS Q8_0 rows [B, Hkv, Sk, 136] for K
+    and V, with the validity rule of ``gather_paged_kv_q8`` (V zeroed, K kept
+    on invalid tokens)."""
+    for t, n in ((key_cache, "key_cache"), (value_cache, "value_cache"),
+                 (block_table, "block_table"), (seq_lens, "seq_lens")):
+        _cuda(t, n)
+    _check(block_table.dtype == torch.int32 and block_table.is_contiguous(),
+           "block_table must be contiguous int32")
+    _check(seq_lens.dtype == torch.int32 and seq_lens.is_contiguous(), "seq_lens must be contiguous int32")
+    bs, Hkv, cbs, chs = _plane_info(key_cache, value_cache)
+    B, M = block_table.shape
+    _check(seq_lens.shape[0] == B, "seq_lens vs block_table batch mismatch")
+    _check(Sk > 0 and Sk % 32 == 0, f"Sk must be positive multiple of 32, got {Sk}")
+
+    def use_or_alloc(buf):
+        if (buf is not None and tuple(buf.shape) == (B, Hkv, Sk, 136) and buf.dtype == torch.uint8
+                and buf.device == key_cache.device and buf.is_contiguous()):
+            return buf
+        return torch.empty((B, Hkv, Sk, 136), dtype=torch.uint8, device=key_cache.device)
+
+    k_o, v_o = use_or_alloc(k_out), use_or_alloc(v_out)
+    err = _load().gfx906_fa_amd_gather_planar(
+        _ptr(key_cache), _ptr(value_cache), _ptr(block_table), _ptr(seq_lens), _ptr(k_o),
+        _ptr(v_o), B, Hkv, Sk, 128, bs, M, cbs, chs, _stream(key_cache.device))
+    _ok(err, "gfx906_fa_amd_gather_planar")
+    return [k_o, v_o]
+
+
+def workspace_size(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int,
+                   max_query_len: int, max_seq_len: int, head_size: int = 128) -> int:
+    return int(_load().gfx906_fa_amd_paged_attention_workspace_size(
+        num_seqs, num_tokens, num_heads, num_kv_heads, head_size, max_query_len, max_seq_len))
+
+
+def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                    block_table: torch.Tensor, seq_lens: torch.Tensor,
+                    query_start_loc: torch.Tensor, max_query_len: int, max_seq_len: int,
+                    scale: float, out: Optional[torch.Tensor] = None,
+                    workspace: Optional[torch.Tensor] = None,
+                    q_abs_offset: Optional[torch.Tensor] = None, causal: bool = True,
+                    out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Varlen direct-paged attention: query [T, Hq, 128] -> out [T, Hq, 128].
+
+    ``max_query_len`` / ``max_seq_len`` must bound the device values (they
+    size the launch; they are host ints so no device sync is needed)."""
+    for t, n in ((query, "query"), (block_table, "block_table"), (seq_lens, "seq_lens"),
+                 (query_start_loc, "query_start_loc")):
+        _cuda(t, n)
+    _check(query.dtype in _DT, "query must be fp16, bf16 or fp32")
+    _check(query.dim() == 3 and query.shape[2] == 128, "query must be [num_tokens, Hq, 128]")
+    _check(query.stride(2) == 1, "query rows must be contiguous")
+    T, Hq, D = query.shape
+    bs, Hkv, cbs, chs = _plane_info(key_cache, value_cache)
+    _check(Hq % Hkv == 0, f"heads_q={Hq} must be divisible by heads_kv={Hkv}")
+    _check(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1,
+           "block_table must be int32 [num_seqs, max_blocks] with contiguous rows")
+    _check(seq_lens.dtype == torch.int32 and seq_lens.is_contiguous(), "seq_lens must be contiguous int32")
+    _check(query_start_loc.dtype == torch.int32 and query_start_loc.is_contiguous(),
+           "query_start_loc must be contiguous int32")
+    B = seq_lens.shape[0]
+    _check(block_table.shape[0] >= B and query_start_loc.shape[0] >= B + 1,
+           "block_table / query_start_loc shorter than seq_lens")
+    if q_abs_offset is not None:
+        _cuda(q_abs_offset, "q_abs_offset")
+        _check(q_abs_offset.dtype == torch.int32 and q_abs_offset.is_contiguous()
+               and q_abs_offset.shape[0] >= B, "q_abs_offset must be int32 [B]")
+    if out is None:
+        out = torch.empty((T, Hq, D), dtype=out_dtype or query.dtype, device=query.device)
+    _cuda(out, "out")
+    _check(out.dtype in _DT and out.dim() == 3 and tuple(out.shape[1:]) == (Hq, D)
+           and out.shape[0] >= T and out.stride(2) == 1, "out must be [num_tokens, Hq, 128] fp32/fp16/bf16")
+    need = workspace_size(B, T, Hq, Hkv, max_query_len, max_seq_len)
+    if need > 0:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
+        _check(workspace.data_ptr() % 256 == 0, "workspace must be 256-byte aligned")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    err = _load().gfx906_fa_amd_paged_attention(
+        _ptr(query), _DT[query.dtype], query.stride(0), query.stride(1), _ptr(key_cache),
+        _ptr(value_cache), cbs, chs, _ptr(block_table), block_table.stride(0), _ptr(seq_lens),
+        _ptr(query_start_loc), _ptr(q_abs_offset), 1 if causal else 0, B, T, Hq, Hkv, D, bs,
+        int(max_query_len), int(max_seq_len), float(scale), _ptr(out), _DT[out.dtype],
+        out.stride(0), out.stride(1), _ptr(workspace) if need > 0 else None, ws_bytes,
+        _stream(query.device))
+    _ok(err, "gfx906_fa_amd_paged_attention")
+    return out
+
+
+def forward_paged_direct(q: torch.Tensor, key_cache_q8: torch.Tensor, value_cache: torch.Tensor,
+                         block_table: torch.Tensor, seq_lens: torch.Tensor, scale: float,
+                         mask: Optional[torch.Tensor] = None,
+                         q_abs_offset: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Padded-batch entry with the reference signature
+    (``extension/gfx906_fa.cpp:516-658``): q [B, Hq, Sq, D] -> fp32
+    [B, Hq, Sq, D].  key_cache_q8 / value_cache are the planar K and V planes
+    of this backend (V is Q8_0 too).  Without q_abs_offset every row sees all
+    seq_lens[b] keys (``kv_max`` cutoff); with it, row j sees keys
+    k <= q_abs_offset[b] + j (inline causal, ``kernel/fattn-q8.cuh:646-653``).
+    A materialised mask is not supported (the reference replaced it with
+    q_abs_offset, ``extension/gfx906_fa_paged.py:400-425``)."""
+    _check(mask is None, "mask is not supported: use q_abs_offset (inline causal)")
+    _cuda(q, "q")
+    _check(q.dim() == 4, "q must be 4D [B, Hq, Sq, D]")
+    B, Hq, Sq, D = q.shape
+    _check(block_table.shape[0] == B, "block_table[0] must equal batch")
+    _check(seq_lens.dim() == 1 and seq_lens.shape[0] == B, "seq_lens must be [batch]")
+    q_bshd = q.transpose(1, 2).reshape(B * Sq, Hq, D)
+    qsl = torch.arange(0, (B + 1) * Sq, Sq, dtype=torch.int32, device=q.device)
+    bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+    max_kv = bt.shape[1] * (key_cache_q8.shape[2] // SUBPAGE_BYTES * SUBPAGE_TOKENS)
+    out = paged_attention(q_bshd, key_cache_q8, value_cache, bt.contiguous(), sl.contiguous(), qsl,
+                          Sq, max_kv, scale, q_abs_offset=q_abs_offset,
+                          causal=q_abs_offset is not None, out_dtype=torch.float32)
+    return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
+
+
+_load()

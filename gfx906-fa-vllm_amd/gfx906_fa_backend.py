@@ -1,0 +1,270 @@
+# SPDX-License-Identifier: Apache-2.0
+"""vLLM v1 attention backend: Q8_0 paged attention on MI355X (gfx950).
+
+Drop-in for ``extension/gfx906_fa_backend.py`` of the reference: same entry
+point (``vllm.general_plugins: gfx906_fa = gfx906_fa_backend:register``,
+reference ``extension/setup.py:56-60``), same registration as
+``AttentionBackendEnum.CUSTOM`` (lines 536-553), same class names and
+``forward`` / ``do_kv_cache_update`` signatures (lines 405-461).
+
+What differs, by design:
+  * K **and** V are stored as Q8_0 (the reference keeps V in fp16 and K in a
+    side buffer that can go stale, lines 277-314 and 428-434).  The Q8 planes
+    live inside vLLM's own per-layer KV tensor, so every write goes through
+    ``do_kv_cache_update`` and there is no second copy to fall out of sync.
+  * ``forward`` makes one varlen HIP call for decode / prefill / mixed /
+    speculative-verify batches and writes ``output`` in place in the model
+    dtype (the reference upcasts Q to fp32, pads, and copies back, lines
+    478-528).
+  * fp16 and bf16 models; head size 128 (the only size the reference's
+    launchers accept, ``extension/gfx906_fa_launcher.cu:76-79``); any block
+    size that is a multiple of 16.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import ClassVar
+
+import torch
+
+from vllm.config import VllmConfig
+from vllm.config.cache import CacheDType
+from vllm.logger import init_logger
+from vllm.platforms.interface import DeviceCapability
+from vllm.v1.attention.backend import (
+    AttentionBackend,
+    AttentionCGSupport,
+    AttentionImpl,
+    AttentionLayer,
+    AttentionMetadataBuilder,
+    AttentionType,
+    CommonAttentionMetadata,
+    MultipleOf,
+)
+from vllm.v1.kv_cache_interface import AttentionSpec
+
+import gfx906_fa
+from gfx906_fa_paged import forward_paged, q8_planes
+
+logger = init_logger(__name__)
+
+
+# -----------------------------------------------------------------------------
+# Metadata (reference lines 59-109)
+# -----------------------------------------------------------------------------
+@dataclass
+class Gfx906FAMetadata:
+    num_actual_tokens: int
+    max_query_len: int
+    max_seq_len: int
+    query_start_loc: torch.Tensor      # [B+1] int32
+    seq_lens: torch.Tensor             # [B]   int32
+    block_table: torch.Tensor          # [B, max_num_blocks] int32
+    slot_mapping: torch.Tensor         # [num_tokens] int64
+    use_cascade: bool = False
+    common_prefix_len: int = 0
+
+
+class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
+    _cudagraph_support: ClassVar[AttentionCGSupport] = AttentionCGSupport.NEVER
+
+    def __init__(self, kv_cache_spec: AttentionSpec, layer_names: list[str],
+                 vllm_config: VllmConfig, device: torch.device):
+        super().__init__(kv_cache_spec, layer_names, vllm_config, device)
+        self.block_size = kv_cache_spec.block_size
+
+    def build_for_cudagraph_capture(self, common_attn_metadata: CommonAttentionMetadata
+                                    ) -> Gfx906FAMetadata:
+        return self.build(0, common_attn_metadata)
+
+    def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
+              fast_build: bool = False) -> Gfx906FAMetadata:
+        return Gfx906FAMetadata(
+            num_actual_tokens=common_attn_metadata.num_actual_tokens,
+            max_query_len=common_attn_metadata.max_query_len,
+            max_seq_len=common_attn_metadata.max_seq_len,
+            query_start_loc=common_attn_metadata.query_start_loc,
+            seq_lens=common_attn_metadata.seq_lens,
+            block_table=common_attn_metadata.block_table_tensor,
+            slot_mapping=common_attn_metadata.slot_mapping,
+            use_cascade=(common_prefix_len > 0),
+            common_prefix_len=common_prefix_len,
+        )
+
+
+# -----------------------------------------------------------------------------
+# Backend (reference lines 115-209)
+# -----------------------------------------------------------------------------
+class Gfx906FABackend(AttentionBackend):
+    accept_output_buffer: bool = True
+
+    supported_dtypes: ClassVar[list[torch.dtype]] = [torch.float16, torch.bfloat16]
+    # vLLM allocates the pages in the model dtype; the Q8_0 planes are stored
+    # inside them (gfx906_fa_paged.q8_planes).
+    supported_kv_cache_dtypes: ClassVar[list[CacheDType]] = ["auto", "float16", "half", "bfloat16"]
+
+    forward_includes_kv_cache_update: bool = False
+
+    @staticmethod
+    def get_supported_kernel_block_sizes() -> list[int | MultipleOf]:
+        return [MultipleOf(16)]
+
+    @classmethod
+    def supports_block_size(cls, block_size: int | None) -> bool:
+        if block_size is None:
+            return True
+        return block_size % 16 == 0
+
+    @staticmethod
+    def get_name() -> str:
+        return "CUSTOM"
+
+    @staticmethod
+    def get_impl_cls() -> type["Gfx906FAImpl"]:
+        return Gfx906FAImpl
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
+                           cache_dtype_str: str = "auto") -> tuple[int, ...]:
+        if block_size % 16 != 0:
+            raise ValueError("Block size must be a multiple of 16.")
+        # Same as TritonAttentionBackend, so the allocator is unchanged.
+        return (num_blocks, 2, block_size, num_kv_heads, head_size)
+
+    @staticmethod
+    def get_kv_cache_stride_order(include_num_layers_dimension: bool = False) -> tuple[int, ...]:
+        if include_num_layers_dimension:
+            return (1, 0, 2, 3, 4, 5)
+        return (0, 1, 2, 3, 4)
+
+    @staticmethod
+    def use_cascade_attention(*args, **kwargs) -> bool:
+        return False
+
+    @staticmethod
+    def get_builder_cls() -> type["Gfx906FAMetadataBuilder"]:
+        return Gfx906FAMetadataBuilder
+
+    @classmethod
+    def supports_head_size(cls, head_size: int) -> bool:
+        return head_size == 128
+
+    @classmethod
+    def supports_mm_prefix(cls) -> bool:
+        return False
+
+    @classmethod
+    def supports_sink(cls) -> bool:
+        return False
+
+    @classmethod
+    def supports_attn_type(cls, attn_type: str) -> bool:
+        return attn_type == AttentionType.DECODER
+
+    @classmethod
+    def supports_alibi_sqrt(cls) -> bool:
+        return False
+
+    @classmethod
+    def supports_compute_capability(cls, capability: DeviceCapability) -> bool:
+        return True
+
+
+# -----------------------------------------------------------------------------
+# Impl (reference lines 215-530)
+# -----------------------------------------------------------------------------
+class Gfx906FAImpl(AttentionImpl):
+    # One split-K workspace per worker, shared by all layers (the reference
+    # shares its gather buffers the same way, lines 229-230).
+    _workspace: ClassVar[torch.Tensor | None] = None
+
+    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
+                 alibi_slopes: list[float] | None, sliding_window: int | None,
+                 kv_cache_dtype: str, logits_soft_cap: float | None = None,
+                 attn_type: AttentionType = AttentionType.DECODER,
+                 kv_sharing_target_layer_name: int | None = None,
+                 sinks: torch.Tensor | None = None, use_alibi_sqrt: bool = False) -> None:
+        if alibi_slopes is not None:
+            raise NotImplementedError("GFX906_FA: alibi_slopes is not supported")
+        if sliding_window is not None:
+            raise NotImplementedError("GFX906_FA: sliding_window is not supported")
+        if logits_soft_cap not in (None, 0, 0.0):
+            raise NotImplementedError("GFX906_FA: logits_soft_cap is not supported")
+        if sinks is not None:
+            raise NotImplementedError("GFX906_FA: sinks are not supported")
+        if attn_type != AttentionType.DECODER:
+            raise NotImplementedError(f"GFX906_FA: attn_type={attn_type} is not supported")
+        if head_size != 128:
+            raise NotImplementedError(f"GFX906_FA: head_size={head_size} is not supported (128 only)")
+        if num_heads % num_kv_heads != 0:
+            raise ValueError("num_heads must be a multiple of num_kv_heads")
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.num_kv_heads = num_kv_heads
+        self.kv_cache_dtype = kv_cache_dtype
+        self.attn_type = attn_type
+        self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+        self.num_queries_per_kv = num_heads // num_kv_heads
+
+    def fused_output_quant_supported(self, quant_key):
+        return False
+
+    def fused_rope_kvcache_supported(self):
+        return False
+
+    @classmethod
+    def _get_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        ws = cls._workspace
+        if ws is None or ws.numel() < nbytes or ws.device != device:
+            cls._workspace = None
+            cls._workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        return cls._workspace
+
+    def do_kv_cache_update(self, layer: AttentionLayer, key: torch.Tensor, value: torch.Tensor,
+                           kv_cache: torch.Tensor, slot_mapping: torch.Tensor):
+        """Quantize K and V of the new tokens to Q8_0 and write them at
+        slot_mapping (< 0 skips) - one launch (reference lines 405-442)."""
+        kp, vp = q8_planes(kv_cache, self.num_kv_heads, self.head_size)
+        n = slot_mapping.shape[0]
+        sm = slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.to(torch.int64)
+        gfx906_fa.reshape_and_cache_q8_kv(key[:n], value[:n], sm, kp, vp)
+
+    def forward(self, layer: torch.nn.Module, query: torch.Tensor, key: torch.Tensor,
+                value: torch.Tensor, kv_cache: torch.Tensor, attn_metadata: Gfx906FAMetadata,
+                output: torch.Tensor | None = None, output_scale: torch.Tensor | None = None,
+                output_block_scale: torch.Tensor | None = None) -> torch.Tensor:
+        assert output is not None, "Output tensor must be provided."
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError("GFX906_FA: output quantization is not supported")
+        if attn_metadata is None:
+            # Profiling run.
+            return output.fill_(0)
+        assert not attn_metadata.use_cascade, "GFX906_FA: cascade is not supported"
+        n = attn_metadata.num_actual_tokens
+        kp, vp = q8_planes(kv_cache, self.num_kv_heads, self.head_size)
+        md = attn_metadata
+        B = md.seq_lens.shape[0]
+        ws = self._get_workspace(
+            gfx906_fa.workspace_size(B, n, self.num_heads, self.num_kv_heads, md.max_query_len,
+                                     md.max_seq_len), query.device)
+        out = output[:n].view(n, self.num_heads, self.head_size)
+        forward_paged(query[:n], kp, vp, md.block_table, md.seq_lens, md.query_start_loc,
+                      md.max_query_len, md.max_seq_len, self.scale, out=out, workspace=ws)
+        return output
+
+
+# -----------------------------------------------------------------------------
+# Registration (reference lines 536-553)
+# -----------------------------------------------------------------------------
+def register() -> None:
+    """Register Gfx906FABackend as AttentionBackendEnum.CUSTOM."""
+    from vllm.v1.attention.backends.registry import AttentionBackendEnum, register_backend
+
+    register_backend(AttentionBackendEnum.CUSTOM, f"{__name__}.Gfx906FABackend")
+    logger.info("GFX906_FA backend registered as AttentionBackendEnum.CUSTOM")
+
+
+register()

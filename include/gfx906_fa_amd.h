@@ -1,0 +1,186 @@
+/* gfx906_fa_amd.h - C ABI of the MI355X (gfx950) Q8_0 paged-attention backend.
+ *
+ * Plain C: pointers, sizes and a hipStream_t.  No allocation, no
+ * synchronisation: every entry point enqueues work on `stream` and returns a
+ * hipError_t (hipErrorInvalidValue plus a line on stderr for an unsupported
+ * configuration, otherwise the launch status).  Citations are to the
+ * reference checkout (nick413-bit/gfx906-fa-vllm).
+ *
+ * Data formats
+ * ------------
+ * Q8_0 block: 32 int8 values plus one fp16 scale (kernel/ggml_shim.cuh:90-94).
+ *   Quantization closed form (extension/gfx906_fa_quant.cu:51-84), per block:
+ *     amax = max|x|; d = amax/127.f; id = d > 0 ? 1.f/d : 0;
+ *     q = clamp(rintf(x*id), -128, 127); scale stored as fp16(d), RNE.
+ *
+ * AoS rows ("block_q8_0 rows"): a row of D values is D/32 blocks of 34 bytes,
+ *   [fp16 d little-endian][32 x int8] each (extension/gfx906_fa_quant.cu:76-84).
+ *
+ * Planar page layout (this backend's KV cache, D = 128): the cache holds two
+ *   planes (K, V).  A page of `block_size` tokens (a multiple of 16) of one
+ *   kv-head in one plane is block_size/16 contiguous 2176-byte sub-pages, each
+ *   covering 16 tokens:
+ *     K sub-page: int8 q[t][d] at t*128 + 32*((d%32)/8) + 8*(d/32) + d%8,
+ *                 fp16 scale[t][b] at 2048 + (4*t + b)*2
+ *     V sub-page: int8 q[t][d] at ((t/4)*16 + d%16)*32 + (d/16)*4 + t%4,
+ *                 fp16 scale[t][b] at 2048 + (4*t + b)*2
+ *   Address of (page p, kv-head h, sub-page j) in a plane:
+ *     plane_base + p*cache_block_stride + h*cache_head_stride + j*2176.
+ *   The values and scales are exactly the Q8_0 blocks of the AoS format;
+ *   only their placement differs (chosen so the attention kernels load MFMA
+ *   operands straight from HBM with aligned 16-byte loads).
+ *
+ * dtype codes: 0 = fp32, 1 = fp16, 2 = bf16.
+ */
+#ifndef GFX906_FA_AMD_H
+#define GFX906_FA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { GFA_DTYPE_F32 = 0, GFA_DTYPE_F16 = 1, GFA_DTYPE_BF16 = 2 };
+
+/* Library version string. */
+const char *gfx906_fa_amd_version(void);
+
+/* ---------------------------------------------------------------------------
+ * (1) Dense Q8_0 quantize of contiguous fp16 rows [N, D] -> AoS rows
+ *     [N, D/32*34].  Same name, arguments and semantics as the reference
+ *     launcher (extension/gfx906_fa_quant.cu:206-223, declared at
+ *     extension/gfx906_fa.cpp:38-44).
+ */
+hipError_t launch_quantize_q8_0_dense(const void *x, uint8_t *y, int N, int D,
+                                      hipStream_t stream);
+
+/* (1b) Same for fp16 / bf16 / fp32 input (x_dtype); N may exceed 2^31 rows
+ *      of blocks.  No reference counterpart: the reference is fp16-only
+ *      (extension/gfx906_fa.cpp:276). */
+hipError_t gfx906_fa_amd_quantize_q8_0(const void *x, int x_dtype, uint8_t *y,
+                                       int64_t N, int D, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (2) Quantize new key rows [T, Hkv, D] (element strides) and scatter them
+ *     as AoS rows into a paged cache [NB, bs, Hkv, D/32*34] (byte strides) at
+ *     slot_mapping[t] (int64; < 0 = skip).  All other bytes are untouched.
+ *     Same name, arguments and semantics as the reference launcher
+ *     (extension/gfx906_fa_quant.cu:225-253, declared at
+ *     extension/gfx906_fa.cpp:46-60); key is fp16.
+ */
+hipError_t launch_reshape_and_cache_q8(const void *key, const int64_t *slot_mapping,
+                                       uint8_t *k_cache_q8, int num_tokens,
+                                       int num_kv_heads, int head_size, int block_size,
+                                       int64_t key_token_stride, int64_t key_head_stride,
+                                       int64_t cache_block_stride,
+                                       int64_t cache_token_stride,
+                                       int64_t cache_head_stride, hipStream_t stream);
+
+/* (2b) Same with an input dtype (fp16 / bf16 / fp32). */
+hipError_t gfx906_fa_amd_reshape_and_cache_q8(
+    const void *key, int key_dtype, const int64_t *slot_mapping, uint8_t *k_cache_q8,
+    int num_tokens, int num_kv_heads, int head_size, int block_size,
+    int64_t key_token_stride, int64_t key_head_stride, int64_t cache_block_stride,
+    int64_t cache_token_stride, int64_t cache_head_stride, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (3) Paged -> contiguous gather.  For s < num_seqs, h < Hkv, t < Sk:
+ *       lb = t / block_size; pb = lb < max_blocks ? block_table[s][lb] : -1;
+ *       if t < seq_lens[s] and pb >= 0: copy the K row (bytes_per_row bytes)
+ *       and the V row (D fp16) of (pb, t % block_size, h);
+ *       else zero the V row and leave the K row untouched.
+ *     Outputs: k_out [B, Hkv, Sk, bytes_per_row], v_out [B, Hkv, Sk, D] fp16.
+ *     K strides in bytes, V strides in fp16 elements.  Same name, arguments
+ *     and semantics as the reference (extension/gfx906_fa_gather.cu:362-425,
+ *     v2 contract at extension/gfx906_fa_gather.cu:190-357, declared at
+ *     extension/gfx906_fa.cpp:94-115).
+ */
+hipError_t launch_gather_paged_kv_q8(
+    const uint8_t *key_cache_q8, const void *value_cache, const int32_t *block_table,
+    const int32_t *seq_lens, uint8_t *k_out, void *v_out, int num_seqs, int num_kv_heads,
+    int Sk, int D, int bytes_per_row, int block_size, int max_blocks_per_seq,
+    int64_t cache_block_stride, int64_t cache_token_stride, int64_t cache_head_stride_q8,
+    int64_t v_cache_block_stride, int64_t v_cache_token_stride,
+    int64_t v_cache_head_stride, hipStream_t stream);
+
+/* (3b) Same contract over generic row byte sizes (k_row_bytes, v_row_bytes;
+ *      all strides in bytes), e.g. an AoS Q8_0 V cache (v_row_bytes = 136):
+ *      the Q8/Q8 variant of (3). */
+hipError_t gfx906_fa_amd_gather_rows(
+    const uint8_t *k_cache, const uint8_t *v_cache, const int32_t *block_table,
+    const int32_t *seq_lens, uint8_t *k_out, uint8_t *v_out, int num_seqs,
+    int num_kv_heads, int Sk, int k_row_bytes, int v_row_bytes, int block_size,
+    int max_blocks_per_seq, int64_t k_block_stride, int64_t k_token_stride,
+    int64_t k_head_stride, int64_t v_block_stride, int64_t v_token_stride,
+    int64_t v_head_stride, hipStream_t stream);
+
+/* (3c) Gather from the planar K+V cache into AoS rows, same validity rule as
+ *      (3): k_out, v_out [B, Hkv, Sk, 136]; invalid tokens get a zero V row
+ *      and an untouched K row.  Replaces the reference's legacy torch gather
+ *      (extension/gfx906_fa_paged.py:148-194) for this cache. */
+hipError_t gfx906_fa_amd_gather_planar(
+    const uint8_t *k_cache, const uint8_t *v_cache, const int32_t *block_table,
+    const int32_t *seq_lens, uint8_t *k_out, uint8_t *v_out, int num_seqs,
+    int num_kv_heads, int Sk, int head_size, int block_size, int max_blocks_per_seq,
+    int64_t cache_block_stride, int64_t cache_head_stride, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (4) Quantize-and-write K and V of new tokens into the planar cache.
+ *     key/value [T, Hkv, D] (element strides, dtype fp16/bf16/fp32, D = 128),
+ *     slot_mapping int64 [T] (< 0 = skip).  Replaces the reference's
+ *     do_kv_cache_update pair (fp16 triton write + K-only Q8 side buffer,
+ *     extension/gfx906_fa_backend.py:405-442; kernel
+ *     extension/gfx906_fa_quant.cu:150-200): one launch, K and V both Q8_0.
+ */
+hipError_t gfx906_fa_amd_cache_write_kv(
+    const void *key, const void *value, int dtype, const int64_t *slot_mapping,
+    uint8_t *k_cache, uint8_t *v_cache, int num_tokens, int num_kv_heads, int head_size,
+    int block_size, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, int64_t cache_block_stride,
+    int64_t cache_head_stride, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (5) Varlen direct-paged attention over the planar Q8 K+V cache: decode,
+ *     chunked prefill, mixed batches and speculative verify in one call.
+ *
+ *     q    [num_tokens, Hq, D] (element strides), dtype fp16/bf16/fp32.
+ *     out  [num_tokens, Hq, D] (element strides), dtype fp32/fp16/bf16.
+ *     Sequence s owns query tokens [query_start_loc[s], query_start_loc[s+1])
+ *     and has seq_lens[s] cached tokens (the new ones included).
+ *     Query row j of s sees keys k < seq_lens[s] with, when causal != 0,
+ *       k <= q_abs_offset[s] + j   (q_abs_offset may be NULL: then
+ *                                   q_abs_offset[s] = seq_lens[s] - n_q[s]).
+ *     q-head hq reads kv-head hq / (Hq/Hkv).  A row with no visible key is 0.
+ *     Numerics: dequantize-then-fp32 softmax (scores, max, sum and output
+ *     accumulated in fp32; K int8 values enter the MFMA exactly and their
+ *     scales are applied to the fp32 products; V scales are folded into P).
+ *     Replaces gfx906_fa_launch_paged (extension/gfx906_fa_launcher.cu:222-352,
+ *     declared at extension/gfx906_fa.cpp:63-90) and the host padding /
+ *     unpadding of extension/gfx906_fa_paged.py:255-330.
+ *     Requirements: D = 128, Hq % Hkv == 0, block_size % 16 == 0, cache
+ *     strides and plane bases 16-byte aligned, workspace of at least
+ *     gfx906_fa_amd_paged_attention_workspace_size(...) bytes (256-byte
+ *     aligned; may be NULL when that size is 0).
+ */
+size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int num_tokens,
+                                                    int num_heads, int num_kv_heads,
+                                                    int head_size, int max_query_len,
+                                                    int max_seq_len);
+
+hipError_t gfx906_fa_amd_paged_attention(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
+    int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *q_abs_offset,
+    int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
+    int head_size, int block_size, int max_query_len, int max_seq_len, float scale,
+    void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
+    void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GFX906_FA_AMD_H */

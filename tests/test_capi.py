@@ -1,0 +1,73 @@
+"""CPU: the C-ABI library loads and exports every entry point the header
+declares; argument validation fails before any GPU work (no compute calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gfx906_fa_amd.h")
+LIB = os.path.join(ROOT, "gfx906-fa-vllm_amd", "libgfx906_fa_amd.so")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", src)) -
+                  {"extern", "if", "defined"})
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    for n in ["launch_quantize_q8_0_dense", "launch_reshape_and_cache_q8",
+              "launch_gather_paged_kv_q8", "gfx906_fa_amd_cache_write_kv",
+              "gfx906_fa_amd_paged_attention", "gfx906_fa_amd_paged_attention_workspace_size",
+              "gfx906_fa_amd_gather_planar", "gfx906_fa_amd_gather_rows"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(LIB), "build the library first (__graft_entry__.build())"
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_validation_errors_without_gpu():
+    import gfx906_fa  # loads the library; no GPU needed
+    L = gfx906_fa.lib()
+    assert b"gfx950" in L.gfx906_fa_amd_version()
+    # head_size 64 is rejected before any launch (hipErrorInvalidValue = 1)
+    err = L.gfx906_fa_amd_paged_attention(None, 1, 0, 0, None, None, 0, 0, None, 0, None, None,
+                                          None, 1, 1, 1, 8, 1, 64, 16, 1, 16, 0.1, None, 1, 0, 0,
+                                          None, 0, None)
+    assert err == 1
+    # block size not a multiple of 16
+    err = L.gfx906_fa_amd_paged_attention(None, 1, 0, 0, None, None, 0, 0, None, 0, None, None,
+                                          None, 1, 1, 1, 8, 1, 128, 24, 1, 16, 0.1, None, 1, 0, 0,
+                                          None, 0, None)
+    assert err == 1
+    # quantize: D not a multiple of 32
+    assert L.gfx906_fa_amd_quantize_q8_0(None, 1, None, 4, 48, None) == 1
+    # planar write: head size must be 128
+    assert L.gfx906_fa_amd_cache_write_kv(None, None, 1, None, None, None, 1, 1, 64, 16,
+                                          0, 0, 0, 0, 0, 0, None) == 1
+    # empty work is a no-op success
+    assert L.gfx906_fa_amd_quantize_q8_0(None, 1, None, 0, 128, None) == 0
+
+
+def test_workspace_size_plan():
+    import gfx906_fa
+    # single split -> no workspace
+    assert gfx906_fa.workspace_size(1, 1, 8, 1, 1, 1024) == 0
+    # long contexts need split partials
+    ws = gfx906_fa.workspace_size(32, 32, 48, 8, 1, 16384)
+    assert ws > 0 and ws % 256 == 0
+
+
+def test_ops_reject_cpu_tensors():
+    import torch
+    import gfx906_fa
+    with pytest.raises(RuntimeError, match="CUDA/HIP"):
+        gfx906_fa.quantize_q8_0(torch.zeros(4, 32, dtype=torch.float16))

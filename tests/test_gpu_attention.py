@@ -1,0 +1,255 @@
+"""GPU: direct-paged attention vs the dequantize-then-float64 oracle.
+
+Tolerance (north star): max-abs 2e-3 and relative Frobenius error 1e-2 for
+fp32 outputs; fp16 / bf16 outputs additionally allow their own rounding
+(2^-11 / 2^-8 of |ref|).  Cases follow the reference's tests:
+decode batches (tests/test_decode_batch.py, test_direct_paged_bitexact.py),
+inline-causal chunked prefill (tests/test_inline_causal.py), mixed batches
+and the TP-8 shard (tests/test_fa_mixed_batch.py), the backend end to end
+(tests/test_backend.py), plus split-K, GQA, block sizes, dtypes, empty
+sequences, and full-size configurations checked on sampled rows and by
+block-table permutation invariance."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import gfx906_fa
+import gfx906_fa_workloads as W
+from gpu_common import announce, assert_close, batch_oracle, need_gpu, to_np_f32
+from oracle import q8_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ROUND = {torch.float32: 0.0, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}
+
+
+def _run_and_check(b, out_dtype=torch.float32, rows=None):
+    announce(f"attention B={b.num_seqs} T={b.num_tokens} Hq={b.Hq} Hkv={b.Hkv} bs={b.block_size} "
+             f"max_q={b.max_query_len} max_k={b.max_seq_len} {b.dtype}->{out_dtype}")
+    out = W.attention(b, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref = batch_oracle(b, rows=rows)
+    got = to_np_f32(out)
+    if rows is not None:
+        got, ref = got[rows], ref[rows]
+    assert_close(got, ref, extra=ROUND[out_dtype])
+    return out
+
+
+def test_golden_cfg1():
+    """The committed cfg1 fixture: cache bytes bit-exact, output in tolerance."""
+    need_gpu()
+    announce("golden cfg1")
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "q8_cfg1.npz"))
+    nb, bs = int(g["num_blocks"]), int(g["block_size"])
+    cache = gfx906_fa.new_kv_cache(nb, bs, 1, device=DEV)
+    key = torch.from_numpy(g["key"]).to(DEV)
+    val = torch.from_numpy(g["value"]).to(DEV)
+    gfx906_fa.reshape_and_cache_q8_kv(key, val, torch.from_numpy(g["slot_mapping"]).to(DEV),
+                                      cache[:, 0], cache[:, 1])
+    assert np.array_equal(cache.cpu().numpy(), g["cache"])
+    q = torch.from_numpy(g["query"]).to(DEV)
+    out = gfx906_fa.paged_attention(q, cache[:, 0], cache[:, 1], torch.from_numpy(g["block_table"]).to(DEV),
+                                    torch.from_numpy(g["seq_lens"]).to(DEV),
+                                    torch.from_numpy(g["query_start_loc"]).to(DEV), 1, 1024,
+                                    1.0 / math.sqrt(128), out_dtype=torch.float32)
+    assert_close(to_np_f32(out), g["out"])
+
+
+@pytest.mark.parametrize("heads", [(8, 1), (48, 8), (32, 4), (16, 16)])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_decode_batch(heads, dt):
+    need_gpu()
+    hq, hkv = heads
+    b = W.build_batch([1, 15, 16, 17, 300, 1000, 2049], [1] * 7, hq, hkv, dtype=dt, seed=1)
+    _run_and_check(b)
+
+
+def test_decode_split_k_long():
+    """Long contexts force several splits and the combine kernel."""
+    need_gpu()
+    b = W.build_batch([20000, 777, 12345], [1] * 3, 8, 1, seed=2)
+    _run_and_check(b)
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_decode_block_sizes(bs):
+    need_gpu()
+    b = W.build_batch([5, 100, 1500], [1] * 3, 12, 2, block_size=bs, seed=3)
+    _run_and_check(b)
+
+
+def test_inline_causal_chunked_prefill():
+    """tests/test_inline_causal.py: 8/2 heads, seq 512/384, chunks 256/128."""
+    need_gpu()
+    b = W.build_batch([512, 384], [256, 128], 8, 2, seed=4)
+    _run_and_check(b)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_full_prefill(dt):
+    need_gpu()
+    b = W.build_batch([300, 77], [300, 77], 12, 2, dtype=dt, seed=5)
+    _run_and_check(b)
+
+
+def test_mixed_batch():
+    need_gpu()
+    sl = [64, 700, 1500, 33, 4000, 9]
+    ql = [64, 200, 1, 1, 1, 9]
+    b = W.build_batch(sl, ql, 48, 8, seed=6)
+    _run_and_check(b)
+
+
+@pytest.mark.parametrize("heads", [(6, 1), (48, 8)])
+def test_spec_verify(heads):
+    """5 verify tokens causal among themselves (G*5 = 30 rows)."""
+    need_gpu()
+    b = W.build_batch([3000, 5, 1200], [5, 5, 5], heads[0], heads[1], seed=7)
+    _run_and_check(b)
+
+
+def test_verify_more_rows_than_decode_tile():
+    """n_q*G = 48 > 32 rows goes to the prefill kernel."""
+    need_gpu()
+    b = W.build_batch([900, 40], [8, 8], 6, 1, seed=8)
+    _run_and_check(b)
+
+
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16])
+def test_output_dtypes(odt):
+    need_gpu()
+    b = W.build_batch([100, 2000], [1, 50], 16, 2, seed=9)
+    _run_and_check(b, out_dtype=odt)
+
+
+def test_fp32_query():
+    need_gpu()
+    b = W.build_batch([260, 31], [1, 31], 8, 2, dtype="f32", seed=10)
+    _run_and_check(b)
+
+
+def test_empty_sequences():
+    """seq_len 0 -> zeros; a sequence with no query tokens writes nothing."""
+    need_gpu()
+    announce("empty sequences")
+    b = W.build_batch([50, 0, 30, 20], [1, 1, 0, 2], 8, 2, seed=11)
+    sentinel = torch.full((b.num_tokens, 8, 128), 7.0, device=DEV)
+    out = W.attention(b, out=sentinel)
+    torch.cuda.synchronize()
+    ref = batch_oracle(b)
+    o = to_np_f32(out)
+    assert not o[1].any()           # token of the seq_len 0 sequence
+    assert_close(o, ref)
+
+
+def test_forward_paged_direct_padded():
+    """Reference-signature padded entry: non-causal (kv_max cutoff) and
+    inline-causal via q_abs_offset (extension/gfx906_fa.cpp:516-658)."""
+    need_gpu()
+    announce("forward_paged_direct")
+    b = W.build_batch([40, 200, 77], [1, 1, 1], 8, 2, seed=12)
+    B, Sq = 3, 4
+    q = torch.randn((B, 8, Sq, 128), device=DEV, dtype=torch.float32)
+    kp, vp = b.planes()
+    out = gfx906_fa.forward_paged_direct(q, kp, vp, b.block_table, b.seq_lens_t, b.scale)
+    qo = torch.tensor([30, 100, 73], dtype=torch.int32, device=DEV)
+    outc = gfx906_fa.forward_paged_direct(q, kp, vp, b.block_table, b.seq_lens_t, b.scale, q_abs_offset=qo)
+    torch.cuda.synchronize()
+    cache = b.kv_cache.cpu().numpy()
+    kh, vh = O.planar_dequant(cache)
+    qn = q.cpu().numpy()
+    for s in range(B):
+        for j in range(Sq):
+            for causal, o in ((False, out), (True, outc)):
+                lim = (int(qo[s]) + j + 1) if causal else int(b.seq_lens[s])
+                lim = min(lim, int(b.seq_lens[s]))
+                ref = O.paged_attention_ref(qn[s, :, j][None], kh, vh, b.block_table_np[s:s + 1],
+                                            np.array([lim], np.int32), np.array([0, 1], np.int32), b.scale)
+                assert_close(o[s, :, j].cpu().numpy(), ref[0])
+
+
+def test_backend_impl_end_to_end():
+    """tests/test_backend.py:60-162 with the vllm stub: do_kv_cache_update then
+    forward on a vLLM-shaped [NB, 2, bs, Hkv, D] fp16 cache."""
+    need_gpu()
+    announce("backend impl end to end")
+    from gfx906_fa_backend import Gfx906FAImpl, Gfx906FAMetadata
+    Hq, Hkv, D, bs, NB = 8, 4, 128, 16, 8
+    Sk = 64
+    torch.manual_seed(0)
+    kv = torch.zeros((NB, 2, bs, Hkv, D), dtype=torch.float16, device=DEV)
+    impl = Gfx906FAImpl(Hq, D, 1 / math.sqrt(D), Hkv, None, None, "auto")
+    bt = torch.tensor([[3, 0, 6, 1]], dtype=torch.int32, device=DEV)
+    pos = torch.arange(Sk, device=DEV)
+    slots = (bt[0, pos // bs].long() * bs + pos % bs)
+    keys = torch.randn((Sk, Hkv, D), dtype=torch.float16, device=DEV)
+    vals = torch.randn((Sk, Hkv, D), dtype=torch.float16, device=DEV)
+    impl.do_kv_cache_update(None, keys[:-1], vals[:-1], kv, slots[:-1])   # prefix
+    impl.do_kv_cache_update(None, keys[-1:], vals[-1:], kv, slots[-1:])   # the decode token
+    q = torch.randn((1, Hq, D), dtype=torch.float16, device=DEV)
+    md = Gfx906FAMetadata(num_actual_tokens=1, max_query_len=1, max_seq_len=Sk,
+                          query_start_loc=torch.tensor([0, 1], dtype=torch.int32, device=DEV),
+                          seq_lens=torch.tensor([Sk], dtype=torch.int32, device=DEV),
+                          block_table=bt, slot_mapping=slots[-1:])
+    output = torch.empty((1, Hq * D), dtype=torch.float16, device=DEV)
+    res = impl.forward(None, q, keys[-1:], vals[-1:], kv, md, output=output)
+    torch.cuda.synchronize()
+    assert res is output
+    kq = O.dequantize_q8_0_rows(O.quantize_q8_0_rows(keys.cpu().numpy()), 128)
+    vq = O.dequantize_q8_0_rows(O.quantize_q8_0_rows(vals.cpu().numpy()), 128)
+    qn = q.float().cpu().numpy()
+    ref = np.zeros((Hq, D))
+    for h in range(Hq):
+        sc = kq[:, h // 2] @ qn[0, h] / math.sqrt(D)
+        p = np.exp(sc - sc.max())
+        ref[h] = p @ vq[:, h // 2] / p.sum()
+    assert_close(output.float().cpu().numpy().reshape(Hq, D), ref, extra=2.0 ** -11)
+
+
+# ---------------------------------------------------------------------------
+# Full-size configurations: sampled-row parity + permutation invariance
+# ---------------------------------------------------------------------------
+def _permuted_copy(b, seed=99):
+    """Same logical cache with its pages shuffled and the table remapped:
+    the output must be bit-identical."""
+    rng = np.random.default_rng(seed)
+    perm = torch.from_numpy(rng.permutation(b.num_blocks)).to(DEV)
+    inv = torch.argsort(perm)
+    cache2 = b.kv_cache[perm]                       # new page i holds old page perm[i]
+    bt = b.block_table.long()
+    bt2 = torch.where(bt >= 0, inv[bt.clamp(min=0)], bt).to(torch.int32)
+    return cache2, bt2
+
+
+@pytest.mark.parametrize("name", ["cfg2", "cfg5"])
+def test_full_size_decode_configs(name):
+    need_gpu()
+    b = W.build_cfg(name, device=DEV)
+    sample = sorted(set(np.linspace(0, b.num_tokens - 1, 6).astype(int).tolist()))
+    out = _run_and_check(b, rows=sample)
+    announce(f"{name} permutation invariance")
+    cache2, bt2 = _permuted_copy(b)
+    out2 = gfx906_fa.paged_attention(b.query, cache2[:, 0], cache2[:, 1], bt2, b.seq_lens_t, b.qsl_t,
+                                     b.max_query_len, b.max_seq_len, b.scale, out_dtype=out.dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_full_size_prefill_cfg3():
+    need_gpu()
+    b = W.build_cfg("cfg3", device=DEV)
+    T = b.num_tokens
+    sample = [0, 1, 15, 16, 17, 1000, 4097, T // 2, T - 2, T - 1]
+    _run_and_check(b, out_dtype=torch.float32, rows=sample)
+
+
+def test_full_size_mixed_cfg4():
+    need_gpu()
+    b = W.build_cfg("cfg4", device=DEV)
+    qsl = b.qsl
+    sample = [0, 2047, 2048 + 5, 3 * 2048 + 2047] + [int(qsl[4 + i]) for i in (0, 17, 59)]
+    _run_and_check(b, rows=sample)

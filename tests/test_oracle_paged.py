@@ -1,0 +1,192 @@
+"""CPU: pin the oracle's cache write, gather, planar layout and attention.
+
+Cache write: invariants of tests/test_quant.py:80-149 (written rows equal the
+dense quantizer, untouched bytes stay, slot < 0 skips) plus the C
+restatement.  Gather: a brute-force per-token loop is compared with a
+vectorised fancy-index version written like tests/test_gather.py:15-38
+(``_ref_gather``) and with the C restatement; edge cases seq_len = 0,
+block_table = -1, Sk beyond the table.  Attention: float64 torch SDPA (math
+path) on the same dequantized inputs, and closed-form cases."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle as C
+from oracle import q8_oracle as O
+
+
+def test_reshape_and_cache_invariants():
+    rng = np.random.default_rng(0)
+    NB, bs, Hkv, D = 10, 16, 4, 128
+    slots = np.array([5, 10, 20, 21, 22], np.int64)
+    key = (rng.standard_normal((5, Hkv, D)) * 0.3).astype(np.float16)
+    cache = np.zeros((NB, bs, Hkv, 136), np.uint8)
+    O.reshape_and_cache_q8_aos(key, slots, cache)
+    dense = O.quantize_q8_0_rows(key)
+    for i, s in enumerate(slots):
+        assert np.array_equal(cache[s // bs, s % bs], dense[i])
+    mask = np.ones((NB, bs), bool)
+    mask[slots // bs, slots % bs] = False
+    assert not cache[mask].any()
+    c2 = np.zeros_like(cache)
+    C.reshape_and_cache(key, slots, c2)
+    assert np.array_equal(cache, c2)
+
+
+def test_reshape_and_cache_skip_negative_slot():
+    rng = np.random.default_rng(1)
+    key = rng.standard_normal((3, 2, 64)).astype(np.float16)
+    cache = np.zeros((4, 16, 2, 68), np.uint8)
+    O.reshape_and_cache_q8_aos(key, np.array([0, -1, 5]), cache)
+    dense = O.quantize_q8_0_rows(key)
+    assert np.array_equal(cache[0, 0], dense[0]) and np.array_equal(cache[0, 5], dense[2])
+    cache[0, 0] = 0
+    cache[0, 5] = 0
+    assert not cache.any()
+
+
+def _fancy_gather(kc, vc, bt, sl, Sk):
+    """Vectorised form in the style of tests/test_gather.py:15-38, plus the
+    table-bound rule of the v2 kernel (a logical block past the table or a
+    -1 entry reads as invalid)."""
+    B, M = bt.shape
+    NB, bs, Hkv, _ = kc.shape
+    t = np.arange(Sk)
+    lb = t // bs
+    pb = np.where(lb[None, :] < M, bt[:, np.minimum(lb, M - 1)], -1)      # [B, Sk]
+    valid = (t[None, :] < sl[:, None]) & (pb >= 0)
+    pbc = np.where(valid, pb, 0)
+    k = kc[pbc, (t % bs)[None, :]]                                       # [B, Sk, Hkv, kb]
+    v = vc[pbc, (t % bs)[None, :]]
+    v = np.where(valid[..., None, None], v, 0)
+    return np.transpose(k, (0, 2, 1, 3)), np.transpose(v, (0, 2, 1, 3)), valid
+
+
+@pytest.mark.parametrize("vdt", ["f16", "q8"])
+def test_gather_three_ways(vdt):
+    rng = np.random.default_rng(2)
+    NB, bs, Hkv, D = 8, 16, 2, 64
+    kc = rng.integers(0, 256, (NB, bs, Hkv, 68), dtype=np.uint8)
+    if vdt == "f16":
+        vc = rng.standard_normal((NB, bs, Hkv, D)).astype(np.float16)
+    else:
+        vc = rng.integers(0, 256, (NB, bs, Hkv, 68), dtype=np.uint8)
+    bt = rng.integers(0, NB, (4, 4)).astype(np.int32)
+    bt[3, 2] = -1
+    sl = np.array([0, 30, 64, 60], np.int32)
+    Sk = 96  # beyond M * bs = 64: those tokens are invalid
+    sentinel = np.full((4, Hkv, Sk, 68), 0xAB, np.uint8)
+    k1, v1 = O.gather_paged_kv_q8_aos(kc, vc, bt, sl, Sk, k_out=sentinel.copy())
+    k2, v2, valid = _fancy_gather(kc, vc, bt, sl, Sk)
+    k3, v3 = C.gather(kc, vc, bt, sl, Sk, k_out=sentinel.copy())
+    assert np.array_equal(v1, v2) and np.array_equal(v1, v3)
+    assert np.array_equal(k1, k3)
+    vb = np.transpose(valid[:, None, :].repeat(Hkv, 1), (0, 1, 2))
+    assert np.array_equal(k1[vb], k2[vb])
+    assert np.all(k1[~vb] == 0xAB)  # K untouched on invalid tokens
+
+
+def test_planar_roundtrip_and_layout():
+    rng = np.random.default_rng(3)
+    bs, Hkv = 32, 3
+    seq = 50
+    k = rng.standard_normal((seq, Hkv, 128)).astype(np.float16)
+    v = rng.standard_normal((seq, Hkv, 128)).astype(np.float16)
+    bt = rng.permutation(6)[:2].astype(np.int32)
+    pos = np.arange(seq)
+    slots = bt[pos // bs].astype(np.int64) * bs + pos % bs
+    cache = np.zeros(O.planar_cache_shape(6, bs, Hkv), np.uint8)
+    O.planar_cache_write(k, v, slots, cache)
+    ka, va = O.planar_to_aos(cache)
+    kaos = np.zeros((6, bs, Hkv, 136), np.uint8)
+    vaos = np.zeros_like(kaos)
+    O.reshape_and_cache_q8_aos(k, slots, kaos)
+    O.reshape_and_cache_q8_aos(v, slots, vaos)
+    assert np.array_equal(ka, kaos) and np.array_equal(va, vaos)
+    # positions are a bijection onto the 2048 int bytes of a sub-page
+    tt, dd = np.meshgrid(np.arange(16), np.arange(128), indexing="ij")
+    kp = (tt * 128 + O.planar_kpos(dd)).ravel()
+    vp = O.planar_vpos(tt, dd).ravel()
+    assert sorted(kp.tolist()) == list(range(2048)) and sorted(vp.tolist()) == list(range(2048))
+    # V: the 4 tokens of a lane group are adjacent bytes for every d
+    assert np.all(np.diff(O.planar_vpos(np.arange(4), 5)) == 1)
+
+
+def _sdpa_ref(query, k_hat, v_hat, bt, sl, qsl, scale):
+    """float64 torch SDPA (math backend) per sequence, GQA by repeat_interleave."""
+    T, Hq, D = query.shape
+    NB, bs, Hkv, _ = k_hat.shape
+    out = torch.zeros((T, Hq, D), dtype=torch.float64)
+    for s in range(len(sl)):
+        q0, q1 = int(qsl[s]), int(qsl[s + 1])
+        n, L = q1 - q0, int(sl[s])
+        if n == 0 or L == 0:
+            continue
+        pos = np.arange(L)
+        K = torch.from_numpy(k_hat[bt[s, pos // bs], pos % bs]).double()      # [L, Hkv, D]
+        V = torch.from_numpy(v_hat[bt[s, pos // bs], pos % bs]).double()
+        K = K.repeat_interleave(Hq // Hkv, dim=1).permute(1, 0, 2)
+        V = V.repeat_interleave(Hq // Hkv, dim=1).permute(1, 0, 2)
+        q = torch.from_numpy(query[q0:q1]).double().permute(1, 0, 2)
+        mask = torch.arange(L)[None, :] <= (L - n + torch.arange(n))[:, None]
+        o = torch.nn.functional.scaled_dot_product_attention(q[None], K[None], V[None],
+                                                             attn_mask=mask[None, None], scale=scale)
+        out[q0:q1] = o[0].permute(1, 0, 2)
+    return out.numpy()
+
+
+def _random_paged(rng, seq_lens, q_lens, Hq, Hkv, bs):
+    bt, nb = O.make_block_table(rng, seq_lens, bs)
+    k = rng.standard_normal((nb, bs, Hkv, 128)).astype(np.float16)
+    v = rng.standard_normal((nb, bs, Hkv, 128)).astype(np.float16)
+    kq = O.dequantize_q8_0_rows(O.quantize_q8_0_rows(k), 128)
+    vq = O.dequantize_q8_0_rows(O.quantize_q8_0_rows(v), 128)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    q = rng.standard_normal((int(qsl[-1]), Hq, 128)).astype(np.float32)
+    return q, kq, vq, bt, np.asarray(seq_lens, np.int32), qsl
+
+
+def test_attention_oracle_matches_sdpa():
+    rng = np.random.default_rng(4)
+    q, kq, vq, bt, sl, qsl = _random_paged(rng, [37, 64, 5, 100], [1, 16, 5, 33], 12, 3, 16)
+    scale = 1 / math.sqrt(128)
+    a = O.paged_attention_ref(q, kq, vq, bt, sl, qsl, scale)
+    b = _sdpa_ref(q, kq, vq, bt, sl, qsl, scale)
+    assert np.max(np.abs(a - b)) < 1e-10
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(5)
+    q, kq, vq, bt, sl, qsl = _random_paged(rng, [1, 20], [1, 20], 4, 2, 16)
+    a = O.paged_attention_ref(q, kq, vq, bt, sl, qsl, 0.1)
+    # single visible key: output = V row (GQA: q-head h reads kv-head h // 2)
+    for h in range(4):
+        assert np.allclose(a[0, h], vq[bt[0, 0], 0, h // 2])
+        assert np.allclose(a[1, h], vq[bt[1, 0], 0, h // 2])  # first prefill row
+    # zero query -> uniform scores -> mean of the visible V rows
+    qz = np.zeros_like(q)
+    az = O.paged_attention_ref(qz, kq, vq, bt, sl, qsl, 0.1)
+    pos = np.arange(20)
+    Vs = vq[bt[1, pos // 16], pos % 16]
+    for j in range(20):
+        assert np.allclose(az[1 + j, 3], Vs[: j + 1, 1].mean(0))
+
+
+def test_attention_invariant_to_page_permutation():
+    rng = np.random.default_rng(6)
+    q, kq, vq, bt, sl, qsl = _random_paged(rng, [70], [3], 4, 1, 16)
+    a = O.paged_attention_ref(q, kq, vq, bt, sl, qsl, 0.2)
+    perm = rng.permutation(kq.shape[0])
+    inv = np.argsort(perm)
+    a2 = O.paged_attention_ref(q, kq[perm], vq[perm], inv[bt].astype(np.int32), sl, qsl, 0.2)
+    assert np.allclose(a, a2, atol=1e-12)
+
+
+def test_empty_rows_are_zero():
+    rng = np.random.default_rng(7)
+    q, kq, vq, bt, sl, qsl = _random_paged(rng, [16, 16], [1, 1], 2, 1, 16)
+    sl = np.array([0, 16], np.int32)
+    a = O.paged_attention_ref(q, kq, vq, bt, sl, qsl, 0.1)
+    assert not a[0].any() and a[1].any()
