@@ -1,0 +1,228 @@
+"""Benchmark of the Q8_0 paged-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-prefill]
+
+Headline (``value``): batched decode, BASELINE cfg2 - 32 sequences with
+contexts U[2048, 16384], 48 query / 8 KV heads, head_dim 128, fp16 Q, Q8_0
+K and V, block_size 16, permuted block tables.  One step = quantize-write the
+32 new tokens' K/V into the paged cache + one attention pass over the batch,
+all inputs resident in HBM.  ``value`` is the algorithmic HBM bytes of a step
+(Q8 K+V of every cached token, Q, O, block-table entries, the new tokens'
+K/V in and Q8 out) divided by the measured step time, in GB/s.
+
+Also reported on the same JSON line:
+  roofline      - attention pass (decode + split combine) algorithmic bytes /
+                  its average duration from HIP events on the launch stream,
+                  against 8 TB/s; ``traffic`` from the committed rocprofv3
+                  FETCH_SIZE/WRITE_SIZE measurement when present.
+  prefill       - cfg3 (32K causal prefill, bf16, 48/8): attention TFLOP/s
+                  (4*D*Hq*sum of visible keys) vs 2.5 PFLOP/s dense fp16/bf16
+                  MFMA peak, and the K/V quantize-write GB/s.
+  cpu_baseline  - the reference's PyTorch CPU path (paged gather + dequantize
+                  + fp32 SDPA, oracle/cpu_baseline.py) on whole cfg2
+                  sequences within a ~15 s budget, same GB/s accounting.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "gfx906-fa-vllm_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _traffic(kernel_tag: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, or None."""
+    p = os.path.join(ROOT, "profiles", f"{kernel_tag}_traffic.json")
+    if os.path.exists(p):
+        try:
+            with open(p) as f:
+                return json.load(f).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def timed(fn, steps: int, warmup: int, inner=None):
+    """Times `steps` calls of fn() with HIP events on the current stream.
+    inner(k) -> (start_event, end_event) pairs recorded inside fn are summed
+    separately when given."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this size (rocprof counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the kernel shards by KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---------------- cfg2 decode -----------------------------------------
+    b = W.build_cfg("cfg2", device=dev)
+    kp, vp = b.planes()
+    B = b.num_seqs
+    # the step's new tokens: the last position of every sequence
+    last = torch.from_numpy(np.cumsum(b.seq_lens.astype(np.int64)) - 1).to(dev)
+    k_new = b.key.index_select(0, last).contiguous()
+    v_new = b.value.index_select(0, last).contiguous()
+    s_new = b.slot_mapping.index_select(0, last).contiguous()
+    out = torch.empty((b.num_tokens, b.Hq, b.D), dtype=torch.float16, device=dev)
+    ws_bytes = gfx906_fa.workspace_size(B, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+
+    attn_ev = []
+
+    def attn():
+        gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t,
+                                  b.max_query_len, b.max_seq_len, b.scale, out=out, workspace=ws)
+
+    def step():
+        gfx906_fa.reshape_and_cache_q8_kv(k_new, v_new, s_new, kp, vp)
+        attn()
+
+    ms_step = timed(step, args.steps, args.warmup)
+    ms_attn = timed(attn, args.steps, args.warmup)
+
+    step_bytes = b.hbm_bytes(out_bytes_per_elem=2) + B * b.Hkv * (2 * 2 * 128 + 2 * 136) + B * 8
+    attn_bytes = b.hbm_bytes(out_bytes_per_elem=2)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    achieved = attn_bytes / (ms_attn * 1e-3) / 1e9
+    traffic = _traffic("attn_decode_cfg2")
+
+    res = {
+        "metric": "Q8 paged decode HBM GB/s (% of peak); causal prefill attn TFLOP/s @32K",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg2 batched decode: 32 seqs, ctx U[2048,16384] (seeded), 48/8 heads, "
+                        "head_dim 128, fp16 Q, Q8_0 K+V, block_size 16, permuted block tables",
+            "num_seqs": B, "total_context": int(b.seq_lens.sum()), "kv_q8_bytes": b.kv_bytes(),
+            "step_bytes": step_bytes, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "attn_decode_kernel+attn_combine_kernel",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic, "algorithmic_bytes": attn_bytes, "avg_us": round(ms_attn * 1e3, 2),
+        },
+    }
+
+    # ---------------- cfg3 prefill (secondary) ------------------------------
+    if not args.no_prefill:
+        del b, out, ws
+        torch.cuda.empty_cache()
+        p = W.build_cfg("cfg3", device=dev)
+        pk, pv = p.planes()
+        pout = torch.empty((p.num_tokens, p.Hq, p.D), dtype=torch.bfloat16, device=dev)
+
+        def pattn():
+            gfx906_fa.paged_attention(p.query, pk, pv, p.block_table, p.seq_lens_t, p.qsl_t,
+                                      p.max_query_len, p.max_seq_len, p.scale, out=pout)
+
+        def pwrite():
+            gfx906_fa.reshape_and_cache_q8_kv(p.key, p.value, p.slot_mapping, pk, pv)
+
+        psteps = max(3, min(10, args.steps // 5))
+        ms_p = timed(pattn, psteps, 2)
+        ms_w = timed(pwrite, psteps, 2)
+        fl = p.flops()
+        wbytes = p.key.numel() * 2 * 2 + p.key.shape[0] * p.Hkv * 2 * 136 + p.key.shape[0] * 8
+        res["prefill"] = {
+            "workload": "cfg3: 1 x 32768 causal prefill from the paged Q8 cache, 48/8, bf16",
+            "attn_ms": round(ms_p, 4), "tflops": round(fl / (ms_p * 1e-3) / 1e12, 2),
+            "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
+            "frac": round(fl / (ms_p * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4), "flop": fl,
+            "kv_write_ms": round(ms_w, 4), "kv_write_gbs": round(wbytes / (ms_w * 1e-3) / 1e9, 1),
+        }
+        del p, pout
+        torch.cuda.empty_cache()
+
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        res["calib_copy_bytes"] = n
+
+    # ---------------- CPU baseline -----------------------------------------
+    if not args.no_cpu:
+        from oracle import cpu_baseline as CB
+        b = W.build_cfg("cfg2", device=dev)
+        cache = b.kv_cache.cpu().numpy()
+        q = b.query.float().cpu()
+        k_aos, v_aos = CB.aos_from_planar(cache)
+        secs, seqs, thr = CB.time_cpu_decode(q, k_aos, v_aos, b.block_table_np, b.seq_lens, b.q_lens,
+                                             b.scale, budget_s=args.cpu_budget)
+        sub_tokens = int(sum(int(b.seq_lens[s]) for s in seqs))
+        sub_bytes = sub_tokens * b.Hkv * 2 * 136 + len(seqs) * b.Hq * b.D * 4
+        res["cpu_baseline"] = {
+            "value": round(sub_bytes / secs / 1e9, 3), "unit": "GB/s", "cores": thr, "kind": "port",
+            "sample": f"cfg2 sequences 0..{seqs[-1]} ({len(seqs)} of {b.num_seqs}, {sub_tokens} cached "
+                      f"tokens): paged gather + dequantize + fp32 SDPA, {secs:.2f} s",
+            "cpu": _cpu_model(),
+        }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

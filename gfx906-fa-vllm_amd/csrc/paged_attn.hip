@@ -38,6 +38,10 @@ using namespace gfa;
 namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr int DEC_DEPTH = 3;   // decode sub-page ring depth
+constexpr int DEC_NW = 4;      // decode waves per workgroup (split the KV range)
+constexpr int PF_NW = 4;       // prefill waves per workgroup
+constexpr int PF_NRG = 2;      // prefill 16-row groups per wave
 constexpr int ROWS_CAP = 32;   // decode partial slots per (seq, kv-head)
 
 struct AttnParams {
@@ -124,7 +128,8 @@ __device__ __forceinline__ void load_subpage(SubPage &sp, const uint8_t *kb, con
 
 __device__ __forceinline__ uint32_t dw(const u32x4 (&v)[2], int i) { return v[i >> 2][i & 3]; }
 
-// Per-wave online-softmax state for NRG groups of 16 rows.
+// Per-wave online-softmax state for NRG groups of 16 rows.  m is in scaled
+// log2 units (score * scale * log2 e).
 template <int NRG>
 struct WaveAcc {
     float4_t o[NRG][8];
@@ -143,74 +148,83 @@ __device__ __forceinline__ void acc_init(WaveAcc<NRG> &a) {
     }
 }
 
-// One k-step: 32 tokens (two sub-pages) starting at tok0 (a multiple of 16).
-// kv_end: exclusive key bound; lim[rg]: inclusive per-row causal bound.
+// Lazy rescaling: the running max m only moves when a row's new max exceeds
+// it by more than LAZY_TAU (log2 units), so O and l are rescaled rarely.
+// p <= 2^LAZY_TAU keeps p * d_v within fp16 range for any fp16 V
+// (d_v <= 65504/127) and for bf16 V with |v| < 1.3e5.
+constexpr float LAZY_TAU = 6.0f;
+
+__device__ __forceinline__ float4_t mfma16k16(half4_t a, half4_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// One 16-token sub-page starting at tok0.
+//   QK: 4 x mfma 16x16x32 (one per Q8 block), K scales on the fp32 products.
+//   PV: 8 x mfma 16x16x16 (one per 16 d); lane (i, g) feeds tokens 4g..4g+3,
+//       the same tokens its S^T fragment holds, so P needs no shuffles.
+// mask (wave-uniform): apply kv_end and the per-row causal bounds lim[rg].
 template <int NRG>
-__device__ __forceinline__ void attend_kstep(WaveAcc<NRG> &acc, const SubPage (&sp)[2],
-                                             const half8_t (&qf)[NRG][4], int tok0, int kv_end,
-                                             const int (&lim)[NRG], float scale_log2e, int g) {
-    // ---- S^T = K Q^T, K scale applied per block -------------------------
-    float s[NRG][8];
+__device__ __forceinline__ void attend_subpage(WaveAcc<NRG> &acc, const SubPage &sp,
+                                               const half8_t (&qf)[NRG][4], int tok0, int kv_end,
+                                               const int (&lim)[NRG], float c, int g, bool mask) {
+    half8_t ka[4];
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
-        half8_t ka[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) ka[b] = i8x8_to_half8(dw(sp[x].kq, 2 * b), dw(sp[x].kq, 2 * b + 1));
-#pragma unroll
-        for (int rg = 0; rg < NRG; ++rg) {
-            float4_t c[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) c[b] = mfma16(ka[b], qf[rg][b], float4_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t s01 = dw(sp[x].ks, 2 * i), s23 = dw(sp[x].ks, 2 * i + 1);
-                float v = c[0][i] * hlo(s01);
-                v = fmaf(c[1][i], hhi(s01), v);
-                v = fmaf(c[2][i], hlo(s23), v);
-                v = fmaf(c[3][i], hhi(s23), v);
-                const int key = tok0 + 16 * x + 4 * g + i;
-                s[rg][4 * x + i] = (key < kv_end && key <= lim[rg]) ? v * scale_log2e : -INFINITY;
-            }
-        }
-    }
-    // ---- online softmax + P'^T ------------------------------------------
+    for (int b = 0; b < 4; ++b) ka[b] = i8x8_to_half8(dw(sp.kq, 2 * b), dw(sp.kq, 2 * b + 1));
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
-        float mt = s[rg][0];
+        float4_t cb[4];
 #pragma unroll
-        for (int e = 1; e < 8; ++e) mt = fmaxf(mt, s[rg][e]);
-        mt = xrow_max(mt);
-        const float mn = fmaxf(acc.m[rg], mt);
-        const float msafe = mn == -INFINITY ? 0.0f : mn;
-        const float alpha = __builtin_amdgcn_exp2f(acc.m[rg] - msafe);
-        acc.m[rg] = mn;
-        float p[8];
-        float ls = 0.0f;
+        for (int b = 0; b < 4; ++b) cb[b] = mfma16(ka[b], qf[rg][b], float4_t{0.f, 0.f, 0.f, 0.f});
+        float sv[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(s[rg][e] - msafe);
-            ls += p[e];
+        for (int i = 0; i < 4; ++i) {  // K scales of token 4g+i: blocks (0,1), (2,3)
+            const uint32_t s01 = dw(sp.ks, 2 * i), s23 = dw(sp.ks, 2 * i + 1);
+            float v = cb[0][i] * hlo(s01);
+            v = fmaf(cb[1][i], hhi(s01), v);
+            v = fmaf(cb[2][i], hlo(s23), v);
+            sv[i] = fmaf(cb[3][i], hhi(s23), v);
         }
-        acc.l[rg] = fmaf(acc.l[rg], alpha, ls);
+        if (mask) {  // uniform: only partial / causal-diagonal sub-pages
 #pragma unroll
-        for (int mm = 0; mm < 8; ++mm) acc.o[rg][mm] *= alpha;
-        // P'_b for the four Q8 blocks of d; token of element e: sub-page e/4,
-        // token 4g + e%4 -> scale dword 2*(e%4) + (b>>1), half b&1.
-        half8_t pb[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t w = dw(sp[e >> 2].vs, 2 * (e & 3) + (b >> 1));
-                const float dv = (b & 1) ? hhi(w) : hlo(w);
-                pb[b][e] = (half_t)(p[e] * dv);
+            for (int i = 0; i < 4; ++i) {
+                const int key = tok0 + 4 * g + i;
+                sv[i] = (key < kv_end && key <= lim[rg]) ? sv[i] : -INFINITY;
             }
         }
-        // ---- O^T += V^T P'^T --------------------------------------------
+        float mt = xrow_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
+        const bool need = mt > acc.m[rg] + LAZY_TAU;
+        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after warm-up
+            const float mn = need ? mt : acc.m[rg];
+            // 0 when m was -inf (nothing accumulated yet); 1 for rows that keep m
+            const float alpha = need ? __builtin_amdgcn_exp2f(acc.m[rg] - mn) : 1.0f;
+            acc.m[rg] = mn;
+            acc.l[rg] *= alpha;
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm) acc.o[rg][mm] *= alpha;
+        }
+        const float nms = acc.m[rg] == -INFINITY ? 0.0f : -acc.m[rg];
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c, nms));
+        acc.l[rg] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        // P'_b[i] = p[i] * d_v[4g + i][b] in packed fp16: the V scale table keeps
+        // the four tokens of a lane group adjacent per block, so dword 2b holds
+        // the scales of tokens (4g, 4g+1) and dword 2b+1 those of (4g+2, 4g+3).
+        const half2_t p01 = {(half_t)pr[0], (half_t)pr[1]};
+        const half2_t p23 = {(half_t)pr[2], (half_t)pr[3]};
+        half4_t pb[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const half2_t a = p01 * __builtin_bit_cast(half2_t, dw(sp.vs, 2 * b));
+            const half2_t c2 = p23 * __builtin_bit_cast(half2_t, dw(sp.vs, 2 * b + 1));
+            pb[b] = half4_t{a[0], a[1], c2[0], c2[1]};
+        }
 #pragma unroll
         for (int mm = 0; mm < 8; ++mm) {
-            const half8_t va = i8x8_to_half8(dw(sp[0].vq, mm), dw(sp[1].vq, mm));
-            acc.o[rg][mm] = mfma16(va, pb[mm >> 1], acc.o[rg][mm]);
+            half2_t lo, hi;
+            i8x4_to_f16x4(dw(sp.vq, mm), lo, hi);
+            const half4_t va = {lo[0], lo[1], hi[0], hi[1]};
+            acc.o[rg][mm] = mfma16k16(va, pb[mm >> 1], acc.o[rg][mm]);
         }
     }
 }
@@ -233,51 +247,71 @@ __device__ __forceinline__ void load_rows(const AttnParams &p, int h, int q0, in
         } else {
 #pragma unroll
             for (int b = 0; b < 4; ++b) qf[rg][b] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-            lim[rg] = sl - 1;
+            lim[rg] = INT32_MAX;  // padding rows never limit the unmasked test
         }
     }
 }
 
-// Streams k-steps ks = ks0, ks0 + kstride, ... of [kv_begin, kv_end) with a
-// one-step register prefetch.
-template <int NRG, bool NT>
-__device__ __forceinline__ void stream_kv(WaveAcc<NRG> &acc, const AttnParams &p, int s, int h,
-                                          int kv_begin, int kv_end, int ks0, int kstride,
-                                          const half8_t (&qf)[NRG][4], const int (&lim)[NRG],
-                                          int i16, int g) {
-    const int nks = (kv_end - kv_begin + 31) >> 5;
-    if (ks0 >= nks) return;
+// Streams the keys [wb, we) (wb a multiple of 16) through the wave, two
+// sub-pages per k-step, with register ping-pong prefetch one k-step ahead.
+// Page ids come from a lane-distributed copy of the block table (lane i holds
+// the page of sub-page 64*chunk + i), refreshed one chunk ahead, so no load in
+// the loop depends on another load.
+template <int NRG, bool NT, int DEPTH>
+__device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams &p, int s, int h,
+                                             int wb, int we, const half8_t (&qf)[NRG][4],
+                                             const int (&lim)[NRG], int lane, int i16, int g) {
+    const int nsub = (we - wb + 15) >> 4;
+    if (nsub <= 0) return;
     const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
-    const int64_t hoff = (int64_t)h * p.chs;
-    auto fetch = [&](SubPage (&sp)[2], int ks) {
+    const uint8_t *kbase = p.kc + (int64_t)h * p.chs;
+    const uint8_t *vbase = p.vc + (int64_t)h * p.chs;
+    const int bs = p.block_size;
+    auto load_pg = [&](int chunk) -> int {
+        const int j = 64 * chunk + lane;
+        return j < nsub ? btrow[(wb + 16 * j) / bs] : 0;
+    };
+    int pg_cur = load_pg(0);
+    int pg_nxt = nsub > 64 ? load_pg(1) : 0;
+    int chunk = 0;
+    // smallest causal bound over the wave's real rows: a k-step entirely below
+    // it (and below we) needs no mask
+    int lim_min = lim[0];
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            const int tb = kv_begin + 32 * ks + 16 * x;
-            if (tb < kv_end) {
-                const int lb = tb / p.block_size;
-                const int64_t page = btrow[lb];
-                const int64_t off = page * p.cbs + hoff + (int64_t)((tb - lb * p.block_size) >> 4) * SUBPAGE_BYTES;
-                load_subpage<NT>(sp[x], p.kc + off, p.vc + off, i16, g);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    sp[x].kq[k] = u32x4{0, 0, 0, 0};
-                    sp[x].ks[k] = u32x4{0, 0, 0, 0};
-                    sp[x].vq[k] = u32x4{0, 0, 0, 0};
-                    sp[x].vs[k] = u32x4{0, 0, 0, 0};
-                }
+    for (int rg = 1; rg < NRG; ++rg) lim_min = min(lim_min, lim[rg]);
+    {
+        // wave-wide min (exact in fp32: bounds are clamped to 2^24)
+        const float f = (float)min(lim_min, 1 << 24);
+        lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
+    }
+    const float c = p.scale_log2e;
+
+    auto fetch = [&](SubPage &sp, int j) {
+        if (j < nsub) {
+            if ((j >> 6) != chunk) {  // advance the page-id window (uniform)
+                chunk = j >> 6;
+                pg_cur = pg_nxt;
+                pg_nxt = 64 * (chunk + 1) < nsub ? load_pg(chunk + 1) : 0;
             }
+            const int tb = wb + 16 * j;
+            const int64_t page = __builtin_amdgcn_readlane(pg_cur, j & 63);
+            const int64_t off = page * p.cbs + (int64_t)((tb % bs) >> 4) * SUBPAGE_BYTES;
+            load_subpage<NT>(sp, kbase + off, vbase + off, i16, g);
         }
     };
-    SubPage cur[2], nxt[2];
-    fetch(cur, ks0);
-    for (int ks = ks0; ks < nks; ks += kstride) {
-        const int kn = ks + kstride;
-        if (kn < nks) fetch(nxt, kn);
-        attend_kstep<NRG>(acc, cur, qf, kv_begin + 32 * ks, kv_end, lim, p.scale_log2e, g);
-        if (kn < nks) {
+    // ring of DEPTH sub-page buffers: DEPTH-1 sub-pages in flight while one computes
+    SubPage buf[DEPTH];
 #pragma unroll
-            for (int x = 0; x < 2; ++x) cur[x] = nxt[x];
+    for (int u = 0; u < DEPTH - 1; ++u) fetch(buf[u], u);
+    for (int base = 0; base < nsub; base += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) {
+            const int j = base + u;
+            if (j >= nsub) break;
+            fetch(buf[(u + DEPTH - 1) % DEPTH], j + DEPTH - 1);
+            const int tok0 = wb + 16 * j;
+            attend_subpage<NRG>(acc, buf[u], qf, tok0, we, lim, c, g,
+                                !(tok0 + 16 <= we && tok0 + 15 <= lim_min));
         }
     }
 }
@@ -308,7 +342,11 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnParams p) {
 
     WaveAcc<NRG> acc;
     acc_init(acc);
-    stream_kv<NRG, true>(acc, p, s, h, kv_begin, kv_end, w, NW, qf, lim, i16, g);
+    // wave w streams a contiguous quarter of the split (whole k-steps)
+    const int chunk = ((kv_end - kv_begin + NW - 1) / NW + 31) & ~31;
+    const int wb = min(kv_end, kv_begin + w * chunk);
+    const int we = min(kv_end, wb + chunk);
+    stream_range<NRG, true, DEC_DEPTH>(acc, p, s, h, wb, we, qf, lim, lane, i16, g);
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) acc.l[rg] = xrow_sum(acc.l[rg]);
 
@@ -409,19 +447,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // workgroup x owns rows [64*(NW*x + w), +64) of (seq, kv-head).
 template <int NW, int QDT, int ODT>
 __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnParams p) {
-    constexpr int NRG = 4;
+    constexpr int NRG = PF_NRG;
     const int s = blockIdx.z, h = blockIdx.y;
     const int q0 = p.qsl[s];
     const int nq = p.qsl[s + 1] - q0;
     const int nrows = nq * p.G;
     if (nq <= 0 || nrows <= p.dec_rows_max) return;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row0 = 64 * (NW * blockIdx.x + w);
+    const int row0 = 16 * NRG * (NW * blockIdx.x + w);
     if (row0 >= nrows) return;  // whole wave; no barriers in this kernel
     const int i16 = lane & 15, g = lane >> 4;
     const int sl = p.seq_lens[s];
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int jlast = (min(row0 + 64, nrows) - 1) / p.G;
+    const int jlast = (min(row0 + 16 * NRG, nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
 
     half8_t qf[NRG][4];
@@ -429,7 +467,7 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnParams p) {
     load_rows<NRG, QDT>(p, h, q0, nrows, row0, sl, qa, i16, g, qf, lim);
     WaveAcc<NRG> acc;
     acc_init(acc);
-    stream_kv<NRG, false>(acc, p, s, h, 0, kv_end, 0, 1, qf, lim, i16, g);
+    stream_range<NRG, false, 2>(acc, p, s, h, 0, kv_end, qf, lim, lane, i16, g);
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
         const float l = xrow_sum(acc.l[rg]);
@@ -458,8 +496,6 @@ struct Plan {
     size_t ws_o_floats, ws_ml_floats;
 };
 
-constexpr int DEC_NW = 4;
-constexpr int PF_NW = 4;
 
 Plan make_plan(int num_seqs, int num_heads, int num_kv_heads, int max_query_len, int max_seq_len) {
     Plan pl;
@@ -503,7 +539,7 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
         attn_combine_kernel<ODT><<<dim3(num_kv_heads, num_seqs), 256, 0, stream>>>(p);
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
-        const int tiles = (rows + 64 * PF_NW - 1) / (64 * PF_NW);
+        const int tiles = (rows + 16 * PF_NRG * PF_NW - 1) / (16 * PF_NRG * PF_NW);
         attn_prefill_kernel<PF_NW, QDT, ODT><<<dim3(tiles, num_kv_heads, num_seqs), 64 * PF_NW, 0, stream>>>(p);
     }
     return hipGetLastError();

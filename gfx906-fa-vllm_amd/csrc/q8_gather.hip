@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void gather_planar_kernel(
             const int r = p - b * 34;
             uint8_t byte;
             if (r < 2) {
-                byte = sub[SCALE_OFF + (4 * tl + b) * 2 + r];
+                byte = sub[(plane ? SCALE_OFF + ((tl >> 2) * 4 + b) * 8 + (tl & 3) * 2
+                                  : SCALE_OFF + (4 * tl + b) * 2) + r];
             } else {
                 const int d = 32 * b + (r - 2);
                 const int pos = plane ? ((tl >> 2) * 16 + (d & 15)) * 32 + (d >> 4) * 4 + (tl & 3)

@@ -86,7 +86,8 @@ __global__ __launch_bounds__(256) void q8_reshape_cache_kernel(
 // dims 2l, 2l+1 of K and of V; block b = l/16 is the lane's DPP row.
 //   K ints : u16 store at t*128 + kpos(2l)   (2l, 2l+1 share an 8-group)
 //   V ints : two byte stores at vpos(t, 2l), vpos(t, 2l+1)
-//   scales : lane 16b writes fp16 scale[t][b] of K and of V
+//   scales : lane 16b writes fp16 scale[t][b] of K (at 2048 + (4t+b)*2) and
+//            of V (at 2048 + ((t/4)*4+b)*8 + (t%4)*2)
 template <int DT, bool VEC>
 __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
     const void *__restrict__ key, const void *__restrict__ value,
@@ -129,9 +130,9 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
     vc[base + vrow + (d0 & 15) * 32] = (uint8_t)rv.qa;
     vc[base + vrow + ((d0 + 1) & 15) * 32] = (uint8_t)rv.qb;
     if ((lane & 15) == 0) {
-        const int so = SCALE_OFF + (4 * tt + b) * 2;
-        *reinterpret_cast<uint16_t *>(kc + base + so) = f32_to_half_bits(rk.d);
-        *reinterpret_cast<uint16_t *>(vc + base + so) = f32_to_half_bits(rv.d);
+        *reinterpret_cast<uint16_t *>(kc + base + SCALE_OFF + (4 * tt + b) * 2) = f32_to_half_bits(rk.d);
+        *reinterpret_cast<uint16_t *>(vc + base + SCALE_OFF + ((tt >> 2) * 4 + b) * 8 + (tt & 3) * 2) =
+            f32_to_half_bits(rv.d);
     }
 }
 

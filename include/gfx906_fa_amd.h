@@ -23,7 +23,7 @@
  *     K sub-page: int8 q[t][d] at t*128 + 32*((d%32)/8) + 8*(d/32) + d%8,
  *                 fp16 scale[t][b] at 2048 + (4*t + b)*2
  *     V sub-page: int8 q[t][d] at ((t/4)*16 + d%16)*32 + (d/16)*4 + t%4,
- *                 fp16 scale[t][b] at 2048 + (4*t + b)*2
+ *                 fp16 scale[t][b] at 2048 + ((t/4)*4 + b)*8 + (t%4)*2
  *   Address of (page p, kv-head h, sub-page j) in a plane:
  *     plane_base + p*cache_block_stride + h*cache_head_stride + j*2176.
  *   The values and scales are exactly the Q8_0 blocks of the AoS format;

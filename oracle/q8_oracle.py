@@ -224,7 +224,7 @@ def gather_paged_kv_q8_aos(key_cache_q8: np.ndarray, value_cache: np.ndarray,
 #   K plane: int8 q[t][d] at t*128 + kpos(d);  fp16 d[t][b] at 2048 + (4t+b)*2
 #            kpos(d) = 32*((d%32)//8) + 8*(d//32) + d%8
 #   V plane: int8 q[t][d] at ((t//4)*16 + d%16)*32 + (d//16)*4 + t%4
-#            fp16 d[t][b] at 2048 + (4t+b)*2
+#            fp16 d[t][b] at 2048 + ((t//4)*4 + b)*8 + (t%4)*2
 def planar_kpos(d: np.ndarray) -> np.ndarray:
     d = np.asarray(d)
     return 32 * ((d % 32) // 8) + 8 * (d // 32) + d % 8
@@ -234,6 +234,15 @@ def planar_vpos(t: np.ndarray, d: np.ndarray) -> np.ndarray:
     t = np.asarray(t)
     d = np.asarray(d)
     return ((t // 4) * 16 + d % 16) * 32 + (d // 16) * 4 + t % 4
+
+
+def planar_spos(plane: int, t, b):
+    """Byte offset of fp16 scale (t, b) inside a sub-page."""
+    t = np.asarray(t)
+    b = np.asarray(b)
+    if plane == 0:
+        return 2048 + (4 * t + b) * 2
+    return 2048 + ((t // 4) * 4 + b) * 8 + (t % 4) * 2
 
 
 def planar_cache_shape(num_blocks: int, block_size: int, Hkv: int, D: int = 128):
@@ -253,8 +262,10 @@ def planar_write_rows(cache: np.ndarray, plane: int, page: int, head: int, tok: 
         buf[base + t * 128 + planar_kpos(dd)] = q_row.view(np.uint8)
     else:
         buf[base + planar_vpos(t, dd)] = q_row.view(np.uint8)
-    sc = np.asarray(d_row, dtype="<f2").view(np.uint8)
-    buf[base + 2048 + 8 * t: base + 2048 + 8 * t + 8] = sc
+    sc = np.asarray(d_row, dtype="<f2").view(np.uint8).reshape(4, 2)
+    for b in range(4):
+        o = base + int(planar_spos(plane, t, b))
+        buf[o:o + 2] = sc[b]
 
 
 def planar_read_rows(cache: np.ndarray, plane: int, page: int, head: int, tok: int):
@@ -267,7 +278,8 @@ def planar_read_rows(cache: np.ndarray, plane: int, page: int, head: int, tok: i
         q = buf[base + t * 128 + planar_kpos(dd)].view(np.int8)
     else:
         q = buf[base + planar_vpos(t, dd)].view(np.int8)
-    d = np.ascontiguousarray(buf[base + 2048 + 8 * t: base + 2048 + 8 * t + 8]).view("<f2")
+    so = base + planar_spos(plane, t, np.arange(4))
+    d = np.ascontiguousarray(np.stack([buf[so], buf[so + 1]], axis=-1)).view("<f2").reshape(4)
     return q.copy(), d.copy()
 
 
@@ -302,8 +314,9 @@ def planar_to_aos(cache: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     # vectorised gather of all rows
     kidx = (sp * SUBPAGE_BYTES + t16 * 128)[:, None] + planar_kpos(dd)[None, :]
     vidx = (sp * SUBPAGE_BYTES)[:, None] + planar_vpos(t16[:, None], dd[None, :])
-    sidx = (sp * SUBPAGE_BYTES + 2048 + 8 * t16)[:, None] + np.arange(8)[None, :]
+    bb = np.arange(8) // 2
     for plane, out, idx in ((0, ko, kidx), (1, vo, vidx)):
+        sidx = (sp * SUBPAGE_BYTES)[:, None] + planar_spos(plane, t16[:, None], bb[None, :]) + np.arange(8)[None, :] % 2
         buf = cache[:, plane]                      # [NB, Hkv, nbytes]
         q = buf[:, :, idx]                         # [NB, Hkv, bs, 128]
         s = buf[:, :, sidx]                        # [NB, Hkv, bs, 8]
