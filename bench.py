@@ -117,7 +117,7 @@ def main() -> int:
     s_new = b.slot_mapping.index_select(0, last).contiguous()
     out = torch.empty((b.num_tokens, b.Hq, b.D), dtype=torch.float16, device=dev)
     ws_bytes = gfx906_fa.workspace_size(B, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    ws = gfx906_fa.new_workspace(ws_bytes, dev)
 
     attn_ev = []
 
@@ -172,10 +172,12 @@ def main() -> int:
         p = W.build_cfg("cfg3", device=dev)
         pk, pv = p.planes()
         pout = torch.empty((p.num_tokens, p.Hq, p.D), dtype=torch.bfloat16, device=dev)
+        pws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(
+            p.num_seqs, p.num_tokens, p.Hq, p.Hkv, p.max_query_len, p.max_seq_len), dev)
 
         def pattn():
             gfx906_fa.paged_attention(p.query, pk, pv, p.block_table, p.seq_lens_t, p.qsl_t,
-                                      p.max_query_len, p.max_seq_len, p.scale, out=pout)
+                                      p.max_query_len, p.max_seq_len, p.scale, out=pout, workspace=pws)
 
         def pwrite():
             gfx906_fa.reshape_and_cache_q8_kv(p.key, p.value, p.slot_mapping, pk, pv)

@@ -25,14 +25,17 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    out = os.path.join(HERE, LIB_NAME)
+def build(verbose: bool = False, out: str | None = None, defines=()) -> str:
+    """Compiles csrc/*.hip into `out` (default: the in-tree library).
+    `defines`: extra -D tuning macros (GFA_DEC_DEPTH, GFA_DEC_NW, GFA_SPLIT_WGS)."""
+    out = out or os.path.join(HERE, LIB_NAME)
     tmp = out + ".tmp"
     cmd = [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         # no fast-math: the Q8_0 quantizer needs IEEE division and rint
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
+        *[f"-D{d}" for d in defines],
         *[os.path.join(HERE, "csrc", s) for s in SOURCES],
         "-o", tmp,
     ]

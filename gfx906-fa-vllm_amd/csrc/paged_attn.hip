@@ -5,30 +5,30 @@
 // causal rule kernel/fattn-q8.cuh:646-653, GQA map kernel/fattn-q8.cuh:898-901,
 // kv cutoff extension/gfx906_fa.cpp:595-604) with dequantize-then-fp32 math.
 //
-// Formulation (wave64, v_mfma_f32_16x16x32_f16), everything transposed so a
-// lane owns one query row:
-//   S^T[16 tok x 16 rows] = K[16 tok x 32 d] . Q^T[32 d x 16 rows]   (per Q8 block)
-//   O^T[16 d x 16 rows]  += V^T[16 d x 32 tok] . P'^T[32 tok x 16 rows]
-// Lane l = 16*g + i: row (column of S^T / O^T) i, token group / d group g.
-// K int8 values enter the MFMA exactly (int8 -> fp16 is exact); each Q8 block
-// gets its own MFMA and its fp16 scale multiplies the fp32 product.  V int8
-// values also enter exactly; the V scale d_v[t][b] is folded into P
-// (P'_b[t] = p[t] * d_v[t][b]) for the MFMAs of d-block b.  Softmax statistics
-// and O accumulate in fp32.
+// Formulation (wave64, fp16 MFMA, fp32 accumulation), transposed so a lane
+// owns one query row:
+//   S^T[16 tok x 16 rows] = K[16 tok x 32 d] . Q^T[32 d x 16 rows]
+//       one v_mfma_f32_16x16x32_f16 per Q8 block of d
+//   O^T[16 d x 16 rows]  += V^T[16 d x 16 tok] . P'^T[16 tok x 16 rows]
+//       one v_mfma_f32_16x16x16_f16 per 16 d
+// Lane l = 16*g + i: row i (column of S^T / O^T), token group / d group g.
+// K int8 values enter the MFMA exactly (int8 -> fp16 is exact) and the fp16
+// block scale multiplies the fp32 product.  V int8 values also enter exactly;
+// the V scale d_v[t][b] is folded into P (P'_b[t] = p[t] * d_v[t][b], fp16)
+// for the MFMAs of d-block b.  Softmax statistics and O accumulate in fp32.
 //
 // The planar page layout (include/gfx906_fa_amd.h) makes every operand an
-// aligned 16-byte load straight from HBM: per 16-token sub-page a lane loads
-// 32 B of K ints, 32 B of K scales, 32 B of V ints, 32 B of V scales.
+// aligned 16-byte load straight from HBM, each wave-wide load instruction
+// covering 1 KB contiguous: per 16-token sub-page a lane loads 32 B of K
+// ints, 32 B of K scales, 32 B of V ints and 32 B of V scales.
 //
 // Query rows are GQA-packed: rows of one kv-head are r = j*G + gq (token j,
 // q-head h*G + gq), so one K/V stream serves all G query heads.
 //
-//   attn_decode_kernel   rows <= 16*NRG per (seq, kv-head); KV split across
-//                        the grid (split-K) and across the NW waves of a
-//                        workgroup (merged in LDS); partials merged by
-//                        attn_combine_kernel when a sequence has > 1 split.
-//   attn_prefill_kernel  rows > 32: each wave owns 64 rows and streams the
-//                        causal KV range; no cross-wave state.
+//   attn_decode_kernel   sequences with n_q*G <= 32 rows (decode, verify):
+//                        stream-K over all KV sub-pages, equal share per wave
+//   attn_prefill_kernel  sequences with more rows: each wave owns 32 rows
+//                        and streams their causal KV range
 #include <cstdio>
 
 #include "q8_common.h"
@@ -38,11 +38,19 @@ using namespace gfa;
 namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr int DEC_DEPTH = 3;   // decode sub-page ring depth
-constexpr int DEC_NW = 4;      // decode waves per workgroup (split the KV range)
-constexpr int PF_NW = 4;       // prefill waves per workgroup
-constexpr int PF_NRG = 2;      // prefill 16-row groups per wave
-constexpr int ROWS_CAP = 32;   // decode partial slots per (seq, kv-head)
+// Tuning knobs (compile-time; defaults measured on MI355X).
+#ifndef GFA_DEC_DEPTH
+#define GFA_DEC_DEPTH 2
+#endif
+#ifndef GFA_DEC_NT
+#define GFA_DEC_NT 1
+#endif
+#ifndef GFA_DEC_WPE
+#define GFA_DEC_WPE 3
+#endif
+constexpr int DEC_DEPTH = GFA_DEC_DEPTH;  // decode sub-page ring depth (DEPTH-1 in flight)
+constexpr int PF_NW = 4;                  // prefill waves per workgroup
+constexpr int PF_NRG = 2;                 // prefill 16-row groups per wave
 
 struct AttnParams {
     const void *q;
@@ -57,9 +65,9 @@ struct AttnParams {
     float scale_log2e;
     void *out;
     int64_t o_ts, o_hs;
-    float *ws_o, *ws_ml;
-    int split_len, max_splits;
-    int dec_rows_max;  // rows handled by the decode kernel
+    float *ws_ml, *ws_o;  // partial (m, l) and O per slot row
+    int num_seqs, nwg;    // nwg: decode workgroups (the grid)
+    int dec_rows_max;     // rows handled by the decode kernel
 };
 
 __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
@@ -102,23 +110,39 @@ struct SubPage {
     u32x4 kq[2], ks[2], vq[2], vs[2];
 };
 
+// Per-lane byte offsets of a lane's operands inside a 2176-byte sub-page.
+struct LaneOffsets {
+    uint32_t kq, ks, vq, vs;
+};
+
+__device__ __forceinline__ LaneOffsets lane_offsets(int i16, int g) {
+    LaneOffsets o;
+    o.kq = (4 * i16 + g) * 16;          // K ints of token i16, group g: +0 and +1024
+    o.ks = SCALE_OFF + 32 * g;          // K scales of tokens 4g..4g+3
+    o.vq = (16 * g + i16) * 16;         // V ints, d = 16m + i16, tokens 4g..4g+3: +0 and +1024
+    o.vs = SCALE_OFF + 32 * g;          // V scales of tokens 4g..4g+3
+    return o;
+}
+
+// kb / vb are wave-uniform sub-page bases; lane offsets are 32-bit, so the
+// loads use the scalar-base + vector-offset addressing form.
 template <bool NT>
 __device__ __forceinline__ void load_subpage(SubPage &sp, const uint8_t *kb, const uint8_t *vb,
-                                             int i16, int g) {
-    const u32x4 *k0 = reinterpret_cast<const u32x4 *>(kb + i16 * 128 + 32 * g);
-    const u32x4 *ks = reinterpret_cast<const u32x4 *>(kb + SCALE_OFF + 32 * g);
-    const u32x4 *v0 = reinterpret_cast<const u32x4 *>(vb + (16 * g + i16) * 32);
-    const u32x4 *vs = reinterpret_cast<const u32x4 *>(vb + SCALE_OFF + 32 * g);
+                                             const LaneOffsets &lo) {
+    const u32x4 *k0 = reinterpret_cast<const u32x4 *>(kb + lo.kq);
+    const u32x4 *ks = reinterpret_cast<const u32x4 *>(kb + lo.ks);
+    const u32x4 *v0 = reinterpret_cast<const u32x4 *>(vb + lo.vq);
+    const u32x4 *vs = reinterpret_cast<const u32x4 *>(vb + lo.vs);
     if constexpr (NT) {  // each KV byte is read once: keep it out of the caches
         sp.kq[0] = __builtin_nontemporal_load(k0);
-        sp.kq[1] = __builtin_nontemporal_load(k0 + 1);
+        sp.kq[1] = __builtin_nontemporal_load(k0 + 64);
         sp.vq[0] = __builtin_nontemporal_load(v0);
-        sp.vq[1] = __builtin_nontemporal_load(v0 + 1);
+        sp.vq[1] = __builtin_nontemporal_load(v0 + 64);
     } else {
         sp.kq[0] = k0[0];
-        sp.kq[1] = k0[1];
+        sp.kq[1] = k0[64];
         sp.vq[0] = v0[0];
-        sp.vq[1] = v0[1];
+        sp.vq[1] = v0[64];
     }
     sp.ks[0] = ks[0];
     sp.ks[1] = ks[1];
@@ -257,11 +281,15 @@ __device__ __forceinline__ void load_rows(const AttnParams &p, int h, int q0, in
 // Page ids come from a lane-distributed copy of the block table (lane i holds
 // the page of sub-page 64*chunk + i), refreshed one chunk ahead, so no load in
 // the loop depends on another load.
+// j0 / jstep: the wave takes sub-pages j0, j0 + jstep, ... of the range (the
+// waves of a workgroup interleave over one range).
 template <int NRG, bool NT, int DEPTH>
 __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams &p, int s, int h,
                                              int wb, int we, const half8_t (&qf)[NRG][4],
-                                             const int (&lim)[NRG], int lane, int i16, int g) {
-    const int nsub = (we - wb + 15) >> 4;
+                                             const int (&lim)[NRG], int lane, int i16, int g,
+                                             int j0 = 0, int jstep = 1) {
+    const int nall = (we - wb + 15) >> 4;
+    const int nsub = nall > j0 ? (nall - j0 + jstep - 1) / jstep : 0;  // this wave's sub-pages
     if (nsub <= 0) return;
     const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
     const uint8_t *kbase = p.kc + (int64_t)h * p.chs;
@@ -269,7 +297,7 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
     const int bs = p.block_size;
     auto load_pg = [&](int chunk) -> int {
         const int j = 64 * chunk + lane;
-        return j < nsub ? btrow[(wb + 16 * j) / bs] : 0;
+        return j < nsub ? btrow[(wb + 16 * (j0 + jstep * j)) / bs] : 0;
     };
     int pg_cur = load_pg(0);
     int pg_nxt = nsub > 64 ? load_pg(1) : 0;
@@ -285,6 +313,7 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
         lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
     }
     const float c = p.scale_log2e;
+    const LaneOffsets lo = lane_offsets(i16, g);
 
     auto fetch = [&](SubPage &sp, int j) {
         if (j < nsub) {
@@ -293,10 +322,10 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
                 pg_cur = pg_nxt;
                 pg_nxt = 64 * (chunk + 1) < nsub ? load_pg(chunk + 1) : 0;
             }
-            const int tb = wb + 16 * j;
+            const int tb = wb + 16 * (j0 + jstep * j);
             const int64_t page = __builtin_amdgcn_readlane(pg_cur, j & 63);
             const int64_t off = page * p.cbs + (int64_t)((tb % bs) >> 4) * SUBPAGE_BYTES;
-            load_subpage<NT>(sp, kbase + off, vbase + off, i16, g);
+            load_subpage<NT>(sp, kbase + off, vbase + off, lo);
         }
     };
     // ring of DEPTH sub-page buffers: DEPTH-1 sub-pages in flight while one computes
@@ -307,139 +336,246 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
 #pragma unroll
         for (int u = 0; u < DEPTH; ++u) {
             const int j = base + u;
-            if (j >= nsub) break;
-            fetch(buf[(u + DEPTH - 1) % DEPTH], j + DEPTH - 1);
-            const int tok0 = wb + 16 * j;
-            attend_subpage<NRG>(acc, buf[u], qf, tok0, we, lim, c, g,
-                                !(tok0 + 16 <= we && tok0 + 15 <= lim_min));
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Decode / verify kernel.  grid (max_splits, Hkv, num_seqs), block 64*NW.
-template <int NRG, int NW, int QDT, int ODT>
-__global__ __launch_bounds__(64 * NW) void attn_decode_kernel(AttnParams p) {
-    const int s = blockIdx.z, h = blockIdx.y, split = blockIdx.x;
-    const int q0 = p.qsl[s];
-    const int nq = p.qsl[s + 1] - q0;
-    const int nrows = nq * p.G;
-    if (nq <= 0 || nrows > p.dec_rows_max) return;
-    const int sl = p.seq_lens[s];
-    const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int kv_lim = p.causal ? min(sl, max(qa + nq, 0)) : sl;
-    // never more splits than the workspace holds; the last one takes the rest
-    const int nsplit = min(max(1, (kv_lim + p.split_len - 1) / p.split_len), p.max_splits);
-    if (split >= nsplit) return;
-    const int kv_begin = split * p.split_len;
-    const int kv_end = split == nsplit - 1 ? kv_lim : min(kv_lim, kv_begin + p.split_len);
-
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int i16 = lane & 15, g = lane >> 4;
-    half8_t qf[NRG][4];
-    int lim[NRG];
-    load_rows<NRG, QDT>(p, h, q0, nrows, 0, sl, qa, i16, g, qf, lim);
-
-    WaveAcc<NRG> acc;
-    acc_init(acc);
-    // wave w streams a contiguous quarter of the split (whole k-steps)
-    const int chunk = ((kv_end - kv_begin + NW - 1) / NW + 31) & ~31;
-    const int wb = min(kv_end, kv_begin + w * chunk);
-    const int we = min(kv_end, wb + chunk);
-    stream_range<NRG, true, DEC_DEPTH>(acc, p, s, h, wb, we, qf, lim, lane, i16, g);
-#pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) acc.l[rg] = xrow_sum(acc.l[rg]);
-
-    constexpr int R = 16 * NRG;
-    __shared__ float sm_o[NW][R][128 + 4];
-    __shared__ float sm_m[NW][R], sm_l[NW][R];
-#pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) {
-        const int r = 16 * rg + i16;
-        if (g == 0) {
-            sm_m[w][r] = acc.m[rg];
-            sm_l[w][r] = acc.l[rg];
-        }
-#pragma unroll
-        for (int mm = 0; mm < 8; ++mm)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sm_o[w][r][16 * mm + 4 * g + i] = acc.o[rg][mm][i];
-    }
-    __syncthreads();
-
-    // merge the NW waves; thread -> (row, 4 consecutive d)
-    for (int it = threadIdx.x; it < R * 32; it += 64 * NW) {
-        const int r = it >> 5, d0 = (it & 31) * 4;
-        if (r >= nrows) continue;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) mx = fmaxf(mx, sm_m[k][r]);
-        const float ms = mx == -INFINITY ? 0.0f : mx;
-        float l = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            const float wk = __builtin_amdgcn_exp2f(sm_m[k][r] - ms);
-            l = fmaf(sm_l[k][r], wk, l);
-            o0 = fmaf(sm_o[k][r][d0 + 0], wk, o0);
-            o1 = fmaf(sm_o[k][r][d0 + 1], wk, o1);
-            o2 = fmaf(sm_o[k][r][d0 + 2], wk, o2);
-            o3 = fmaf(sm_o[k][r][d0 + 3], wk, o3);
-        }
-        if (nsplit == 1) {
-            const int j = r / p.G;
-            const int hq = h * p.G + (r - j * p.G);
-            const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
-            const float inv = l > 0.f ? 1.0f / l : 0.0f;
-            store_out<ODT>(p.out, ob + 0, o0 * inv);
-            store_out<ODT>(p.out, ob + 1, o1 * inv);
-            store_out<ODT>(p.out, ob + 2, o2 * inv);
-            store_out<ODT>(p.out, ob + 3, o3 * inv);
-        } else {
-            const int64_t slot = (((int64_t)s * p.Hkv + h) * ROWS_CAP + r) * p.max_splits + split;
-            *reinterpret_cast<float4_t *>(p.ws_o + slot * 128 + d0) = float4_t{o0, o1, o2, o3};
-            if (d0 == 0) {
-                p.ws_ml[2 * slot] = mx;
-                p.ws_ml[2 * slot + 1] = l;
+            if (j < nsub) {  // uniform
+                fetch(buf[(u + DEPTH - 1) % DEPTH], j + DEPTH - 1);
+                const int tok0 = wb + 16 * (j0 + jstep * j);
+                attend_subpage<NRG>(acc, buf[u], qf, tok0, we, lim, c, g,
+                                    !(tok0 + 16 <= we && tok0 + 15 <= lim_min));
             }
         }
     }
 }
 
-// Merge split partials.  grid (Hkv, num_seqs), block 256: thread -> (row, 4 d).
-template <int ODT>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
-    const int s = blockIdx.y, h = blockIdx.x;
-    const int q0 = p.qsl[s];
-    const int nq = p.qsl[s + 1] - q0;
-    const int nrows = nq * p.G;
-    if (nq <= 0 || nrows > p.dec_rows_max) return;
-    const int sl = p.seq_lens[s];
-    const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int kv_lim = p.causal ? min(sl, max(qa + nq, 0)) : sl;
-    const int nsplit = min(max(1, (kv_lim + p.split_len - 1) / p.split_len), p.max_splits);
-    if (nsplit == 1) return;
-    for (int it = threadIdx.x; it < ROWS_CAP * 32; it += 256) {
-        const int r = it >> 5, d0 = (it & 31) * 4;
-        if (r >= nrows) continue;
-        const int64_t slot0 = (((int64_t)s * p.Hkv + h) * ROWS_CAP + r) * p.max_splits;
-        float mx = -INFINITY;
-        for (int k = 0; k < nsplit; ++k) mx = fmaxf(mx, p.ws_ml[2 * (slot0 + k)]);
-        const float ms = mx == -INFINITY ? 0.0f : mx;
-        float l = 0.f;
-        float4_t o = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < nsplit; ++k) {
-            const float wk = __builtin_amdgcn_exp2f(p.ws_ml[2 * (slot0 + k)] - ms);
-            l = fmaf(p.ws_ml[2 * (slot0 + k) + 1], wk, l);
-            const float4_t ok = *reinterpret_cast<const float4_t *>(p.ws_o + (slot0 + k) * 128 + d0);
-            o += ok * wk;
-        }
-        const int j = r / p.G;
-        const int hq = h * p.G + (r - j * p.G);
-        const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
-        const float inv = l > 0.f ? 1.0f / l : 0.0f;
+// ---------------------------------------------------------------------------
+// Decode / speculative-verify kernel (stream-K over workgroups).
+//
+// Work units are the 16-token sub-pages of every (sequence, kv-head) segment
+// whose query rows fit one decode tile (n_q * G <= 16*NRG), ordered
+// sequence-major, kv-head minor.  The grid holds the resident workgroups;
+// workgroup w streams the contiguous unit range [U*w/nwg, U*(w+1)/nwg), so
+// every workgroup gets the same number of bytes whatever the context
+// lengths.  Its four waves interleave over each piece (wave k takes
+// sub-pages k, k+4, ...) and merge their softmax states in LDS at the end of
+// the piece.  A range covers whole segments (written out directly) plus at
+// most one partial piece at each end, stored in the workgroup's two
+// workspace slots and merged by attn_combine_kernel.
+//
+// Register budget: one row group runs GFA_DEC_WPE waves per SIMD; two row
+// groups (speculative verify) need twice the accumulators and run 2.
+constexpr int DEC_NW = 4;          // waves per decode workgroup
+constexpr int DEC_MIN_UNITS = 16;  // sub-pages per decode workgroup, at least
+
+template <int NRG>
+struct DecCfg {
+    static constexpr int depth = NRG == 1 ? DEC_DEPTH : 2;
+    static constexpr int wpe = NRG == 1 ? GFA_DEC_WPE : 2;
+};
+
+struct SegInfo {
+    int q0, nq, sl, qa, kv_lim, nsub;
+};
+
+// Per-sequence decode segment: nsub sub-pages of keys (at least one, so a
+// sequence with no visible key still gets its zero output written), or 0 when
+// the sequence belongs to the prefill kernel.
+__device__ __forceinline__ SegInfo seg_info(const AttnParams &p, int s) {
+    SegInfo si;
+    si.q0 = p.qsl[s];
+    si.nq = p.qsl[s + 1] - si.q0;
+    si.sl = p.seq_lens[s];
+    si.qa = p.q_abs ? p.q_abs[s] : si.sl - si.nq;
+    si.kv_lim = p.causal ? min(si.sl, max(si.qa + si.nq, 0)) : si.sl;
+    const bool dec = si.nq > 0 && si.nq * p.G <= p.dec_rows_max;
+    si.nsub = dec ? max((si.kv_lim + 15) >> 4, 1) : 0;
+    return si;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o);
+        if (lane >= o) v += t;
     }
+    return v;
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    return ((int64_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((int)(v & 0xFFFFFFFF));
+}
+
+// Total decode units U and the number of participating workgroups (every
+// range non-empty and at least DEC_MIN_UNITS long).  Wave-level, uniform.
+__device__ __forceinline__ void dec_total(const AttnParams &p, int lane, int64_t &U, int &nwg) {
+    int64_t tot = 0;
+    for (int base = 0; base < p.num_seqs; base += 64) {
+        const int si = base + lane;
+        const int n = si < p.num_seqs ? seg_info(p, si).nsub : 0;
+        tot += __shfl(wave_incl_scan(n, lane), 63);
+    }
+    U = uniform64(tot * p.Hkv);
+    nwg = (int)max((int64_t)1, min((int64_t)p.nwg, U / DEC_MIN_UNITS));
+}
+
+__device__ __forceinline__ int64_t range_start(int64_t U, int k, int n) { return U * k / n; }
+// the workgroup whose range holds unit u
+__device__ __forceinline__ int range_of(int64_t U, int64_t u, int n) { return (int)(((u + 1) * n - 1) / U); }
+
+template <int NRG, int QDT, int ODT>
+__global__ __launch_bounds__(64 * DEC_NW)
+__attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void attn_decode_kernel(AttnParams p) {
+    constexpr int R = 16 * NRG;  // rows per slot
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i16 = lane & 15, g = lane >> 4;
+    const int B = p.num_seqs, Hkv = p.Hkv;
+    const int w = blockIdx.x;
+
+    int64_t U;
+    int nwg;
+    dec_total(p, lane, U, nwg);
+    if (w >= nwg || U == 0) return;  // uniform over the workgroup
+    const int64_t u0 = range_start(U, w, nwg), u1 = range_start(U, w + 1, nwg);
+    // locate the sequence holding u0 (Ps = sub-pages of the sequences before s)
+    int s = 0;
+    int64_t Ps = 0;
+    for (int base = 0; base < B; base += 64) {
+        const int si = base + lane;
+        const int n = si < B ? seg_info(p, si).nsub : 0;
+        const int incl = wave_incl_scan(n, lane);
+        const int ctot = __shfl(incl, 63);
+        if ((Ps + ctot) * Hkv > u0) {
+            const uint64_t bal = __ballot((Ps + incl) * Hkv > u0);
+            const int i = __builtin_ctzll(bal);
+            s = base + i;
+            Ps += __shfl(incl - n, i);
+            break;
+        }
+        Ps += ctot;
+    }
+    s = __builtin_amdgcn_readfirstlane(s);
+    Ps = uniform64(Ps);
+    SegInfo si = seg_info(p, s);
+
+    __shared__ float sm_o[DEC_NW][R][128 + 4];
+    __shared__ float sm_m[DEC_NW][R], sm_l[DEC_NW][R];
+    int64_t u = u0;
+    bool first = true;
+    while (u < u1) {
+        const int64_t off = u - Ps * Hkv;
+        const int h = (int)(off / si.nsub);
+        const int a = (int)(off - (int64_t)h * si.nsub);
+        const int b = (int)min((int64_t)si.nsub, a + (u1 - u));
+        const int nrows = si.nq * p.G;
+
+        half8_t qf[NRG][4];
+        int lim[NRG];
+        load_rows<NRG, QDT>(p, h, si.q0, nrows, 0, si.sl, si.qa, i16, g, qf, lim);
+        WaveAcc<NRG> acc;
+        acc_init(acc);
+        stream_range<NRG, GFA_DEC_NT != 0, DecCfg<NRG>::depth>(acc, p, s, h, 16 * a,
+                                                                 min(16 * b, si.kv_lim), qf, lim,
+                                                                 lane, i16, g, wv, DEC_NW);
+        // ---- merge the four waves' states in LDS ---------------------------
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg) {
+            const float l = xrow_sum(acc.l[rg]);
+            const int r = 16 * rg + i16;
+            if (g == 0) {
+                sm_m[wv][r] = acc.m[rg];
+                sm_l[wv][r] = l;
+            }
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm)
+                *reinterpret_cast<float4_t *>(&sm_o[wv][r][16 * mm + 4 * g]) = acc.o[rg][mm];
+        }
+        __syncthreads();
+        const bool whole = a == 0 && b == si.nsub;
+        const int slot = 2 * w + (first ? 0 : 1);
+        for (int it = threadIdx.x; it < nrows * 32; it += 64 * DEC_NW) {
+            const int r = it >> 5, d0 = (it & 31) * 4;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < DEC_NW; ++k) mx = fmaxf(mx, sm_m[k][r]);
+            const float ms = mx == -INFINITY ? 0.0f : mx;
+            float l = 0.f;
+            float4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < DEC_NW; ++k) {
+                const float wk = __builtin_amdgcn_exp2f(sm_m[k][r] - ms);
+                l = fmaf(sm_l[k][r], wk, l);
+                o += *reinterpret_cast<const float4_t *>(&sm_o[k][r][d0]) * wk;
+            }
+            if (whole) {
+                const int j = r / p.G;
+                const int hq = h * p.G + (r - j * p.G);
+                const int64_t ob = (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
+                const float inv = l > 0.f ? 1.0f / l : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
+            } else {
+                const int64_t row = (int64_t)slot * R + r;
+                *reinterpret_cast<float4_t *>(p.ws_o + row * 128 + d0) = o;
+                if (d0 == 0) {
+                    p.ws_ml[2 * row] = mx;
+                    p.ws_ml[2 * row + 1] = l;
+                }
+            }
+        }
+        __syncthreads();  // LDS reused by the next piece
+        u += b - a;
+        first = false;
+        if (u < u1 && b == si.nsub && h == Hkv - 1) {  // next sequence with decode work
+            Ps += si.nsub;
+            do {
+                ++s;
+                si = seg_info(p, s);
+            } while (si.nsub == 0 && s + 1 < B);
+        }
+    }
+}
+
+// Merges the partial pieces of split decode segments.  grid (R, Hkv, num_seqs),
+// block 128 (thread = d): one workgroup per (row, segment).
+template <int NRG, int ODT>
+__global__ __launch_bounds__(128) void attn_combine_kernel(AttnParams p) {
+    constexpr int R = 16 * NRG;
+    const int r = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    const SegInfo si = seg_info(p, s);
+    if (si.nsub == 0 || r >= si.nq * p.G) return;
+    const int lane = threadIdx.x & 63;
+    int64_t U;
+    int nwg;
+    dec_total(p, lane, U, nwg);
+    // units before this segment
+    int64_t Ps = 0;
+    for (int base = 0; base < s; base += 64) {
+        const int sj = base + lane;
+        const int n = sj < s ? seg_info(p, sj).nsub : 0;
+        Ps += __shfl(wave_incl_scan(n, lane), 63);
+    }
+    const int64_t S0 = uniform64(Ps) * p.Hkv + (int64_t)h * si.nsub;
+    const int wf = range_of(U, S0, nwg), wl = range_of(U, S0 + si.nsub - 1, nwg);
+    if (wf == wl && range_start(U, wf, nwg) <= S0 && range_start(U, wf + 1, nwg) >= S0 + si.nsub)
+        return;  // whole segment in one workgroup: already written
+    const int d = threadIdx.x;
+    float mx = -INFINITY;
+    for (int k = wf; k <= wl; ++k) {
+        const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
+        mx = fmaxf(mx, p.ws_ml[2 * ((int64_t)sk * R + r)]);
+    }
+    const float ms = mx == -INFINITY ? 0.0f : mx;
+    float l = 0.f, o = 0.f;
+    for (int k = wf; k <= wl; ++k) {
+        const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
+        const int64_t row = (int64_t)sk * R + r;
+        const float wk = __builtin_amdgcn_exp2f(p.ws_ml[2 * row] - ms);
+        l = fmaf(p.ws_ml[2 * row + 1], wk, l);
+        o = fmaf(p.ws_o[row * 128 + d], wk, o);
+    }
+    const int j = r / p.G;
+    const int hq = h * p.G + (r - j * p.G);
+    store_out<ODT>(p.out, (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d, l > 0.f ? o / l : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -453,7 +589,8 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnParams p) {
     const int nq = p.qsl[s + 1] - q0;
     const int nrows = nq * p.G;
     if (nq <= 0 || nrows <= p.dec_rows_max) return;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int row0 = 16 * NRG * (NW * blockIdx.x + w);
     if (row0 >= nrows) return;  // whole wave; no barriers in this kernel
     const int i16 = lane & 15, g = lane >> 4;
@@ -485,58 +622,58 @@ __global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Host-side plan.  Deterministic in the call's scalar arguments so that
-// workspace_size() and the launch agree.
+// Host-side plan.  Deterministic in the call's scalar arguments and the
+// device's CU count, so that workspace_size() and the launch agree.
 struct Plan {
+    int dec_nrg;        // 1 or 2 row groups per decode wave
     int dec_rows_max;   // 16 or 32
-    int dec_nrg;        // 1 or 2
-    int split_len;      // tokens per split, multiple of 32*DEC_NW
-    int max_splits;
+    int nwg;            // decode workgroups (resident workgroups of the device)
     bool need_prefill;
-    size_t ws_o_floats, ws_ml_floats;
+    size_t off_ml, off_o, bytes;  // workspace layout
 };
 
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-Plan make_plan(int num_seqs, int num_heads, int num_kv_heads, int max_query_len, int max_seq_len) {
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+Plan make_plan(int num_seqs, int num_heads, int num_kv_heads, int max_query_len) {
     Plan pl;
     const int G = num_heads / num_kv_heads;
     const int max_rows = max_query_len * G;
     pl.dec_nrg = (max_rows <= 16) ? 1 : 2;
     pl.dec_rows_max = 16 * pl.dec_nrg;
     pl.need_prefill = max_rows > pl.dec_rows_max;
-    // Split-K: aim for ~2048 (seq, kv-head, split) workgroups at the longest
-    // context, keep each split >= 64 tokens per decode row so the partials
-    // stay a few percent of the KV bytes, and round to whole k-steps.
-    const int step = 32 * DEC_NW;
-    int64_t target = ((int64_t)num_seqs * num_kv_heads * (int64_t)max(max_seq_len, 1)) / 2048;
-    int64_t minlen = 64LL * pl.dec_rows_max;
-    int64_t sl = max(target, minlen);
-    sl = ((sl + step - 1) / step) * step;
-    if (sl > (1 << 30)) sl = 1 << 30;
-    pl.split_len = (int)sl;
-    pl.max_splits = max(1, (max_seq_len + pl.split_len - 1) / pl.split_len);
-    if (pl.max_splits > 1) {
-        pl.ws_o_floats = (size_t)num_seqs * num_kv_heads * ROWS_CAP * pl.max_splits * 128;
-        pl.ws_ml_floats = (size_t)num_seqs * num_kv_heads * ROWS_CAP * pl.max_splits * 2;
-    } else {
-        pl.ws_o_floats = pl.ws_ml_floats = 0;
-    }
+    const int wpe = pl.dec_nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe;
+    pl.nwg = device_cus() * 4 * wpe / DEC_NW;
+    const size_t rc = (size_t)pl.dec_rows_max;
+    pl.off_ml = 0;
+    pl.off_o = align256((size_t)2 * pl.nwg * rc * 2 * sizeof(float));
+    pl.bytes = pl.off_o + align256((size_t)2 * pl.nwg * rc * 128 * sizeof(float));
     return pl;
 }
-
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 template <int QDT, int ODT>
 hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int num_kv_heads,
                       int max_query_len, hipStream_t stream) {
     AttnParams p = p0;
-    dim3 dgrid(pl.max_splits, num_kv_heads, num_seqs);
-    if (pl.dec_nrg == 1)
-        attn_decode_kernel<1, DEC_NW, QDT, ODT><<<dgrid, 64 * DEC_NW, 0, stream>>>(p);
-    else
-        attn_decode_kernel<2, DEC_NW, QDT, ODT><<<dgrid, 64 * DEC_NW, 0, stream>>>(p);
-    if (pl.max_splits > 1)
-        attn_combine_kernel<ODT><<<dim3(num_kv_heads, num_seqs), 256, 0, stream>>>(p);
+    if (pl.dec_nrg == 1) {
+        attn_decode_kernel<1, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
+        attn_combine_kernel<1, ODT><<<dim3(16, num_kv_heads, num_seqs), 128, 0, stream>>>(p);
+    } else {
+        attn_decode_kernel<2, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
+        attn_combine_kernel<2, ODT><<<dim3(32, num_kv_heads, num_seqs), 128, 0, stream>>>(p);
+    }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
         const int tiles = (rows + 16 * PF_NRG * PF_NW - 1) / (16 * PF_NRG * PF_NW);
@@ -553,10 +690,9 @@ extern "C" size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int
                                                                int max_seq_len) {
     (void)num_tokens;
     (void)head_size;
+    (void)max_seq_len;
     if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads) return 0;
-    const Plan pl = make_plan(num_seqs, num_heads, num_kv_heads, max(max_query_len, 1), max_seq_len);
-    if (pl.max_splits <= 1) return 0;
-    return align256(pl.ws_o_floats * 4) + align256(pl.ws_ml_floats * 4);
+    return make_plan(num_seqs, num_heads, num_kv_heads, max(max_query_len, 1)).bytes;
 }
 
 extern "C" hipError_t gfx906_fa_amd_paged_attention(
@@ -593,11 +729,10 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
         return hipErrorInvalidValue;
     }
     const int G = num_heads / num_kv_heads;
-    const Plan pl = make_plan(num_seqs, num_heads, num_kv_heads, max(max_query_len, 1), max_seq_len);
-    const size_t need = pl.max_splits > 1 ? align256(pl.ws_o_floats * 4) + align256(pl.ws_ml_floats * 4) : 0;
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u))) {
+    const Plan pl = make_plan(num_seqs, num_heads, num_kv_heads, max(max_query_len, 1));
+    if (workspace == nullptr || workspace_bytes < pl.bytes || ((uintptr_t)workspace & 255u)) {
         fprintf(stderr, "[gfx906_fa_amd] paged_attention: workspace of %zu bytes (256-aligned) required, got %zu\n",
-                need, workspace_bytes);
+                pl.bytes, workspace_bytes);
         return hipErrorInvalidValue;
     }
     AttnParams p;
@@ -621,10 +756,11 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     p.out = out;
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
-    p.ws_o = need ? static_cast<float *>(workspace) : nullptr;
-    p.ws_ml = need ? reinterpret_cast<float *>(static_cast<char *>(workspace) + align256(pl.ws_o_floats * 4)) : nullptr;
-    p.split_len = pl.split_len;
-    p.max_splits = pl.max_splits;
+    char *ws = static_cast<char *>(workspace);
+    p.ws_ml = reinterpret_cast<float *>(ws + pl.off_ml);
+    p.ws_o = reinterpret_cast<float *>(ws + pl.off_o);
+    p.num_seqs = num_seqs;
+    p.nwg = pl.nwg;
     p.dec_rows_max = pl.dec_rows_max;
 
 #define GFA_DISPATCH_O(QDT)                                                                    \

@@ -102,8 +102,10 @@ __global__ __launch_bounds__(256) void gather_planar_kernel(
                                   : SCALE_OFF + (4 * tl + b) * 2) + r];
             } else {
                 const int d = 32 * b + (r - 2);
-                const int pos = plane ? ((tl >> 2) * 16 + (d & 15)) * 32 + (d >> 4) * 4 + (tl & 3)
-                                      : tl * 128 + 32 * ((d & 31) >> 3) + 8 * (d >> 5) + (d & 7);
+                const int pos = plane ? ((d >> 6) * 1024 + ((tl >> 2) * 16 + (d & 15)) * 16 +
+                                         ((d >> 4) & 3) * 4 + (tl & 3))
+                                      : ((d >> 6) * 1024 + (4 * tl + ((d >> 3) & 3)) * 16 +
+                                         ((d >> 5) & 1) * 8 + (d & 7));
                 byte = sub[pos];
             }
             word |= (uint32_t)byte << (8 * k);

@@ -84,8 +84,10 @@ __global__ __launch_bounds__(256) void q8_reshape_cache_kernel(
 // ---------------------------------------------------------------------------
 // Planar K+V write (D = 128).  One wave per (token, kv-head): lane l holds
 // dims 2l, 2l+1 of K and of V; block b = l/16 is the lane's DPP row.
-//   K ints : u16 store at t*128 + kpos(2l)   (2l, 2l+1 share an 8-group)
-//   V ints : two byte stores at vpos(t, 2l), vpos(t, 2l+1)
+//   K ints : u16 store at kpos(t, 2l)   (2l, 2l+1 share an 8-group)
+//            kpos(t, d) = (b/2)*1024 + (4t+g)*16 + (b%2)*8 + d%8, b = d/32, g = (d%32)/8
+//   V ints : byte stores at vpos(t, 2l), vpos(t, 2l+1)
+//            vpos(t, d) = (m/4)*1024 + ((t/4)*16 + d%16)*16 + (m%4)*4 + t%4, m = d/16
 //   scales : lane 16b writes fp16 scale[t][b] of K (at 2048 + (4t+b)*2) and
 //            of V (at 2048 + ((t/4)*4+b)*8 + (t%4)*2)
 template <int DT, bool VEC>
@@ -121,14 +123,14 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
     const Q8Pair rv = q8_quantize_pair(va, vb);
 
     const int b = lane >> 4;
-    // K: kpos(d) = 32*((d%32)/8) + 8*(d/32) + d%8
-    const int kpos = 32 * ((d0 & 31) >> 3) + 8 * (d0 >> 5) + (d0 & 7);
-    *reinterpret_cast<uint16_t *>(kc + base + tt * 128 + kpos) =
+    const int kb2 = d0 >> 5, kg = (d0 >> 3) & 3;
+    const int kpos = (kb2 >> 1) * 1024 + (4 * tt + kg) * 16 + (kb2 & 1) * 8 + (d0 & 7);
+    *reinterpret_cast<uint16_t *>(kc + base + kpos) =
         (uint16_t)((uint8_t)rk.qa | ((uint16_t)(uint8_t)rk.qb << 8));
-    // V: vpos(t, d) = ((t/4)*16 + d%16)*32 + (d/16)*4 + t%4
-    const int vrow = ((tt >> 2) * 16) * 32 + (d0 >> 4) * 4 + (tt & 3);
-    vc[base + vrow + (d0 & 15) * 32] = (uint8_t)rv.qa;
-    vc[base + vrow + ((d0 + 1) & 15) * 32] = (uint8_t)rv.qb;
+    const int m = d0 >> 4;
+    const int vrow = (m >> 2) * 1024 + ((tt >> 2) * 16) * 16 + (m & 3) * 4 + (tt & 3);
+    vc[base + vrow + (d0 & 15) * 16] = (uint8_t)rv.qa;
+    vc[base + vrow + ((d0 + 1) & 15) * 16] = (uint8_t)rv.qb;
     if ((lane & 15) == 0) {
         *reinterpret_cast<uint16_t *>(kc + base + SCALE_OFF + (4 * tt + b) * 2) = f32_to_half_bits(rk.d);
         *reinterpret_cast<uint16_t *>(vc + base + SCALE_OFF + ((tt >> 2) * 4 + b) * 8 + (tt & 3) * 2) =

@@ -33,7 +33,7 @@ from typing import Optional
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libgfx906_fa_amd.so")
+LIB_PATH = os.environ.get("GFX906_FA_AMD_LIB") or os.path.join(_HERE, "libgfx906_fa_amd.so")
 
 QK8_0 = 32
 Q8_0_BYTES = 34
@@ -302,6 +302,13 @@ def gather_paged_kv_q8q8(key_cache: torch.Tensor, value_cache: torch.Tensor,
     return [k_o, v_o]
 
 
+def new_workspace(nbytes: int, device) -> torch.Tensor:
+    """Attention workspace: zero-filled once (its per-segment counters must
+    start at 0; every call leaves them at 0).  Reuse it across calls on one
+    stream; calls that overlap on different streams need their own."""
+    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
 def workspace_size(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int,
                    max_query_len: int, max_seq_len: int, head_size: int = 128) -> int:
     return int(_load().gfx906_fa_amd_paged_attention_workspace_size(
@@ -346,17 +353,16 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     _check(out.dtype in _DT and out.dim() == 3 and tuple(out.shape[1:]) == (Hq, D)
            and out.shape[0] >= T and out.stride(2) == 1, "out must be [num_tokens, Hq, 128] fp32/fp16/bf16")
     need = workspace_size(B, T, Hq, Hkv, max_query_len, max_seq_len)
-    if need > 0:
-        if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
-        _check(workspace.data_ptr() % 256 == 0, "workspace must be 256-byte aligned")
-    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = new_workspace(need, query.device)
+    _check(workspace.data_ptr() % 256 == 0, "workspace must be 256-byte aligned")
+    ws_bytes = workspace.numel() * workspace.element_size()
     err = _load().gfx906_fa_amd_paged_attention(
         _ptr(query), _DT[query.dtype], query.stride(0), query.stride(1), _ptr(key_cache),
         _ptr(value_cache), cbs, chs, _ptr(block_table), block_table.stride(0), _ptr(seq_lens),
         _ptr(query_start_loc), _ptr(q_abs_offset), 1 if causal else 0, B, T, Hq, Hkv, D, bs,
         int(max_query_len), int(max_seq_len), float(scale), _ptr(out), _DT[out.dtype],
-        out.stride(0), out.stride(1), _ptr(workspace) if need > 0 else None, ws_bytes,
+        out.stride(0), out.stride(1), _ptr(workspace), ws_bytes,
         _stream(query.device))
     _ok(err, "gfx906_fa_amd_paged_attention")
     return out

@@ -174,8 +174,9 @@ class Gfx906FABackend(AttentionBackend):
 # Impl (reference lines 215-530)
 # -----------------------------------------------------------------------------
 class Gfx906FAImpl(AttentionImpl):
-    # One split-K workspace per worker, shared by all layers (the reference
-    # shares its gather buffers the same way, lines 229-230).
+    # One attention workspace per worker, shared by all layers (the reference
+    # shares its gather buffers the same way, lines 229-230).  Layers run in
+    # order on one stream, so reuse is safe.
     _workspace: ClassVar[torch.Tensor | None] = None
 
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
@@ -215,12 +216,10 @@ class Gfx906FAImpl(AttentionImpl):
 
     @classmethod
     def _get_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor | None:
-        if nbytes == 0:
-            return None
         ws = cls._workspace
         if ws is None or ws.numel() < nbytes or ws.device != device:
             cls._workspace = None
-            cls._workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            cls._workspace = gfx906_fa.new_workspace(nbytes, device)
         return cls._workspace
 
     def do_kv_cache_update(self, layer: AttentionLayer, key: torch.Tensor, value: torch.Tensor,

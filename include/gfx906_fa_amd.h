@@ -20,9 +20,11 @@
  *   planes (K, V).  A page of `block_size` tokens (a multiple of 16) of one
  *   kv-head in one plane is block_size/16 contiguous 2176-byte sub-pages, each
  *   covering 16 tokens:
- *     K sub-page: int8 q[t][d] at t*128 + 32*((d%32)/8) + 8*(d/32) + d%8,
+ *     K sub-page: int8 q[t][d] at (b/2)*1024 + (4t+g)*16 + (b%2)*8 + d%8
+ *                 (b = d/32, g = (d%32)/8),
  *                 fp16 scale[t][b] at 2048 + (4*t + b)*2
- *     V sub-page: int8 q[t][d] at ((t/4)*16 + d%16)*32 + (d/16)*4 + t%4,
+ *     V sub-page: int8 q[t][d] at (m/4)*1024 + ((t/4)*16 + d%16)*16 + (m%4)*4 + t%4
+ *                 (m = d/16),
  *                 fp16 scale[t][b] at 2048 + ((t/4)*4 + b)*8 + (t%4)*2
  *   Address of (page p, kv-head h, sub-page j) in a plane:
  *     plane_base + p*cache_block_stride + h*cache_head_stride + j*2176.
@@ -161,9 +163,15 @@ hipError_t gfx906_fa_amd_cache_write_kv(
  *     declared at extension/gfx906_fa.cpp:63-90) and the host padding /
  *     unpadding of extension/gfx906_fa_paged.py:255-330.
  *     Requirements: D = 128, Hq % Hkv == 0, block_size % 16 == 0, cache
- *     strides and plane bases 16-byte aligned, workspace of at least
- *     gfx906_fa_amd_paged_attention_workspace_size(...) bytes (256-byte
- *     aligned; may be NULL when that size is 0).
+ *     strides and plane bases 16-byte aligned, max_query_len >= every n_q
+ *     (it sizes the prefill grid; max_seq_len is advisory), and a workspace
+ *     of at least gfx906_fa_amd_paged_attention_workspace_size(...) bytes,
+ *     256-byte aligned and ZERO-FILLED before its first use (it holds
+ *     per-(sequence, kv-head) counters that every call returns to zero).
+ *     Calls sharing one workspace must be ordered (same stream).
+ *     Decode-shaped sequences (n_q*Hq/Hkv <= 32 rows) are split stream-K
+ *     style: the device's resident waves each stream an equal share of all
+ *     their KV sub-pages, merging split segments in the workspace.
  */
 size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int num_tokens,
                                                     int num_heads, int num_kv_heads,

@@ -221,19 +221,26 @@ def gather_paged_kv_q8_aos(key_cache_q8: np.ndarray, value_cache: np.ndarray,
 # Planar MFMA page layout of this build (D = 128)
 # ---------------------------------------------------------------------------
 # Per (page, kv-head) each 16-token sub-page is 2176 bytes:
-#   K plane: int8 q[t][d] at t*128 + kpos(d);  fp16 d[t][b] at 2048 + (4t+b)*2
-#            kpos(d) = 32*((d%32)//8) + 8*(d//32) + d%8
-#   V plane: int8 q[t][d] at ((t//4)*16 + d%16)*32 + (d//16)*4 + t%4
+#   K plane: int8 q[t][d] at kpos(t, d), with b = d//32, g = (d%32)//8:
+#              kpos = (b//2)*1024 + (4t + g)*16 + (b%2)*8 + d%8
+#            fp16 d[t][b] at 2048 + (4t+b)*2
+#   V plane: int8 q[t][d] at vpos(t, d), with m = d//16:
+#              vpos = (m//4)*1024 + ((t//4)*16 + d%16)*16 + (m%4)*4 + t%4
 #            fp16 d[t][b] at 2048 + ((t//4)*4 + b)*8 + (t%4)*2
-def planar_kpos(d: np.ndarray) -> np.ndarray:
-    d = np.asarray(d)
-    return 32 * ((d % 32) // 8) + 8 * (d // 32) + d % 8
-
-
-def planar_vpos(t: np.ndarray, d: np.ndarray) -> np.ndarray:
+# Each half (1024 bytes) of the int area is what one wave-wide 16-byte load
+# instruction reads, fully contiguous.
+def planar_kpos(t, d) -> np.ndarray:
     t = np.asarray(t)
     d = np.asarray(d)
-    return ((t // 4) * 16 + d % 16) * 32 + (d // 16) * 4 + t % 4
+    b, g = d // 32, (d % 32) // 8
+    return (b // 2) * 1024 + (4 * t + g) * 16 + (b % 2) * 8 + d % 8
+
+
+def planar_vpos(t, d) -> np.ndarray:
+    t = np.asarray(t)
+    d = np.asarray(d)
+    m = d // 16
+    return (m // 4) * 1024 + ((t // 4) * 16 + d % 16) * 16 + (m % 4) * 4 + t % 4
 
 
 def planar_spos(plane: int, t, b):
@@ -259,7 +266,7 @@ def planar_write_rows(cache: np.ndarray, plane: int, page: int, head: int, tok: 
     dd = np.arange(128)
     buf = cache[page, plane, head]
     if plane == 0:
-        buf[base + t * 128 + planar_kpos(dd)] = q_row.view(np.uint8)
+        buf[base + planar_kpos(t, dd)] = q_row.view(np.uint8)
     else:
         buf[base + planar_vpos(t, dd)] = q_row.view(np.uint8)
     sc = np.asarray(d_row, dtype="<f2").view(np.uint8).reshape(4, 2)
@@ -275,7 +282,7 @@ def planar_read_rows(cache: np.ndarray, plane: int, page: int, head: int, tok: i
     dd = np.arange(128)
     buf = cache[page, plane, head]
     if plane == 0:
-        q = buf[base + t * 128 + planar_kpos(dd)].view(np.int8)
+        q = buf[base + planar_kpos(t, dd)].view(np.int8)
     else:
         q = buf[base + planar_vpos(t, dd)].view(np.int8)
     so = base + planar_spos(plane, t, np.arange(4))
@@ -312,7 +319,7 @@ def planar_to_aos(cache: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     sp, t16 = tt // PAGE_TOKENS, tt % PAGE_TOKENS
     dd = np.arange(128)
     # vectorised gather of all rows
-    kidx = (sp * SUBPAGE_BYTES + t16 * 128)[:, None] + planar_kpos(dd)[None, :]
+    kidx = (sp * SUBPAGE_BYTES)[:, None] + planar_kpos(t16[:, None], dd[None, :])
     vidx = (sp * SUBPAGE_BYTES)[:, None] + planar_vpos(t16[:, None], dd[None, :])
     bb = np.arange(8) // 2
     for plane, out, idx in ((0, ko, kidx), (1, vo, vidx)):

@@ -107,11 +107,15 @@ def test_planar_roundtrip_and_layout():
     assert np.array_equal(ka, kaos) and np.array_equal(va, vaos)
     # positions are a bijection onto the 2048 int bytes of a sub-page
     tt, dd = np.meshgrid(np.arange(16), np.arange(128), indexing="ij")
-    kp = (tt * 128 + O.planar_kpos(dd)).ravel()
+    kp = O.planar_kpos(tt, dd).ravel()
     vp = O.planar_vpos(tt, dd).ravel()
     assert sorted(kp.tolist()) == list(range(2048)) and sorted(vp.tolist()) == list(range(2048))
     # V: the 4 tokens of a lane group are adjacent bytes for every d
     assert np.all(np.diff(O.planar_vpos(np.arange(4), 5)) == 1)
+    # each 16-byte chunk of a lane's MFMA operand: K lane (t, g) reads
+    # (4t+g)*16 and 1024 + (4t+g)*16 -> the 64 lanes cover each 1 KB half
+    ko = sorted({int(O.planar_kpos(t, 8 * g)) // 16 for t in range(16) for g in range(4)})
+    assert ko == list(range(64))
 
 
 def _sdpa_ref(query, k_hat, v_hat, bt, sl, qsl, scale):
