@@ -64,19 +64,20 @@ def _traffic(kernel_tag: str):
     return None
 
 
-def timed(fn, steps: int, warmup: int, inner=None):
-    """Times `steps` calls of fn() with HIP events on the current stream.
-    inner(k) -> (start_event, end_event) pairs recorded inside fn are summed
-    separately when given."""
+def timed(fn, steps: int, warmup: int):
+    """Average ms of fn() over `steps` calls, from HIP events recorded on the
+    stream the kernels are launched on (the library launches on torch's
+    current stream), after `warmup` untimed calls."""
     import torch
+    stream = torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
+    s.record(stream)
     for _ in range(steps):
         fn()
-    e.record()
+    e.record(stream)
     torch.cuda.synchronize()
     return s.elapsed_time(e) / steps
 
@@ -118,8 +119,6 @@ def main() -> int:
     out = torch.empty((b.num_tokens, b.Hq, b.D), dtype=torch.float16, device=dev)
     ws_bytes = gfx906_fa.workspace_size(B, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
     ws = gfx906_fa.new_workspace(ws_bytes, dev)
-
-    attn_ev = []
 
     def attn():
         gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t,
@@ -198,10 +197,12 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     if args.calib_copy_mib:
+        # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE
+        # readings scale the attention kernels' counters to bytes
         n = args.calib_copy_mib << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        src = torch.empty(n // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
         res["calib_copy_bytes"] = n
 

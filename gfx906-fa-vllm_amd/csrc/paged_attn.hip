@@ -66,6 +66,8 @@ struct AttnParams {
     void *out;
     int64_t o_ts, o_hs;
     float *ws_ml, *ws_o;  // partial (m, l) and O per slot row
+    int64_t *ws_hdr;      // decode plan published for the combine kernel: U, nwg
+    int *ws_pre;          // per-sequence exclusive prefix of decode sub-pages
     int num_seqs, nwg;    // nwg: decode workgroups (the grid)
     int dec_rows_max;     // rows handled by the decode kernel
 };
@@ -434,6 +436,22 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     int64_t U;
     int nwg;
     dec_total(p, lane, U, nwg);
+    if (w == 0 && wv == 0) {
+        // publish the plan for attn_combine_kernel: U, nwg, per-sequence
+        // exclusive prefix of decode sub-pages
+        int64_t run = 0;
+        for (int base = 0; base < B; base += 64) {
+            const int sj = base + lane;
+            const int n = sj < B ? seg_info(p, sj).nsub : 0;
+            const int incl = wave_incl_scan(n, lane);
+            if (sj < B) p.ws_pre[sj] = (int)run + incl - n;
+            run += __shfl(incl, 63);
+        }
+        if (lane == 0) {
+            p.ws_hdr[0] = U;
+            p.ws_hdr[1] = nwg;
+        }
+    }
     if (w >= nwg || U == 0) return;  // uniform over the workgroup
     const int64_t u0 = range_start(U, w, nwg), u1 = range_start(U, w + 1, nwg);
     // locate the sequence holding u0 (Ps = sub-pages of the sequences before s)
@@ -535,47 +553,48 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     }
 }
 
-// Merges the partial pieces of split decode segments.  grid (R, Hkv, num_seqs),
-// block 128 (thread = d): one workgroup per (row, segment).
+// Merges the partial pieces of split decode segments, from the plan the
+// decode kernel published (U, nwg, per-sequence prefix).  grid (num_seqs, Hkv),
+// block 256: thread -> (row, 4 consecutive d); one-pass online merge, so the
+// loads of all pieces are independent.
 template <int NRG, int ODT>
-__global__ __launch_bounds__(128) void attn_combine_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     constexpr int R = 16 * NRG;
-    const int r = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+    const int s = blockIdx.x, h = blockIdx.y;
     const SegInfo si = seg_info(p, s);
-    if (si.nsub == 0 || r >= si.nq * p.G) return;
-    const int lane = threadIdx.x & 63;
-    int64_t U;
-    int nwg;
-    dec_total(p, lane, U, nwg);
-    // units before this segment
-    int64_t Ps = 0;
-    for (int base = 0; base < s; base += 64) {
-        const int sj = base + lane;
-        const int n = sj < s ? seg_info(p, sj).nsub : 0;
-        Ps += __shfl(wave_incl_scan(n, lane), 63);
-    }
-    const int64_t S0 = uniform64(Ps) * p.Hkv + (int64_t)h * si.nsub;
+    const int64_t U = p.ws_hdr[0];
+    const int nwg = (int)p.ws_hdr[1];
+    const int pre = p.ws_pre[s];
+    if (si.nsub == 0 || U == 0) return;
+    const int64_t S0 = (int64_t)pre * p.Hkv + (int64_t)h * si.nsub;
     const int wf = range_of(U, S0, nwg), wl = range_of(U, S0 + si.nsub - 1, nwg);
     if (wf == wl && range_start(U, wf, nwg) <= S0 && range_start(U, wf + 1, nwg) >= S0 + si.nsub)
         return;  // whole segment in one workgroup: already written
-    const int d = threadIdx.x;
-    float mx = -INFINITY;
-    for (int k = wf; k <= wl; ++k) {
-        const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
-        mx = fmaxf(mx, p.ws_ml[2 * ((int64_t)sk * R + r)]);
+    const int nrows = si.nq * p.G;
+    for (int it = threadIdx.x; it < nrows * 32; it += 256) {
+        const int r = it >> 5, d0 = (it & 31) * 4;
+        float m = -INFINITY, l = 0.f;
+        float4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int k = wf; k <= wl; ++k) {
+            const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
+            const int64_t row = (int64_t)sk * R + r;
+            const float mk = p.ws_ml[2 * row], lk = p.ws_ml[2 * row + 1];
+            const float4_t ok = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
+            const float mn = fmaxf(m, mk);
+            const float ms = mn == -INFINITY ? 0.0f : mn;
+            const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
+            l = l * a + lk * c;
+            o = o * a + ok * c;
+            m = mn;
+        }
+        const int j = r / p.G;
+        const int hq = h * p.G + (r - j * p.G);
+        const int64_t ob = (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
+        const float inv = l > 0.f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
     }
-    const float ms = mx == -INFINITY ? 0.0f : mx;
-    float l = 0.f, o = 0.f;
-    for (int k = wf; k <= wl; ++k) {
-        const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
-        const int64_t row = (int64_t)sk * R + r;
-        const float wk = __builtin_amdgcn_exp2f(p.ws_ml[2 * row] - ms);
-        l = fmaf(p.ws_ml[2 * row + 1], wk, l);
-        o = fmaf(p.ws_o[row * 128 + d], wk, o);
-    }
-    const int j = r / p.G;
-    const int hq = h * p.G + (r - j * p.G);
-    store_out<ODT>(p.out, (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d, l > 0.f ? o / l : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -629,7 +648,7 @@ struct Plan {
     int dec_rows_max;   // 16 or 32
     int nwg;            // decode workgroups (resident workgroups of the device)
     bool need_prefill;
-    size_t off_ml, off_o, bytes;  // workspace layout
+    size_t off_hdr, off_pre, off_ml, off_o, bytes;  // workspace layout
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -657,8 +676,10 @@ Plan make_plan(int num_seqs, int num_heads, int num_kv_heads, int max_query_len)
     const int wpe = pl.dec_nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe;
     pl.nwg = device_cus() * 4 * wpe / DEC_NW;
     const size_t rc = (size_t)pl.dec_rows_max;
-    pl.off_ml = 0;
-    pl.off_o = align256((size_t)2 * pl.nwg * rc * 2 * sizeof(float));
+    pl.off_hdr = 0;
+    pl.off_pre = 256;
+    pl.off_ml = pl.off_pre + align256((size_t)num_seqs * sizeof(int));
+    pl.off_o = pl.off_ml + align256((size_t)2 * pl.nwg * rc * 2 * sizeof(float));
     pl.bytes = pl.off_o + align256((size_t)2 * pl.nwg * rc * 128 * sizeof(float));
     return pl;
 }
@@ -669,10 +690,10 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     AttnParams p = p0;
     if (pl.dec_nrg == 1) {
         attn_decode_kernel<1, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<1, ODT><<<dim3(16, num_kv_heads, num_seqs), 128, 0, stream>>>(p);
+        attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(p);
     } else {
         attn_decode_kernel<2, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<2, ODT><<<dim3(32, num_kv_heads, num_seqs), 128, 0, stream>>>(p);
+        attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(p);
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
@@ -757,6 +778,8 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
     char *ws = static_cast<char *>(workspace);
+    p.ws_hdr = reinterpret_cast<int64_t *>(ws + pl.off_hdr);
+    p.ws_pre = reinterpret_cast<int *>(ws + pl.off_pre);
     p.ws_ml = reinterpret_cast<float *>(ws + pl.off_ml);
     p.ws_o = reinterpret_cast<float *>(ws + pl.off_o);
     p.num_seqs = num_seqs;

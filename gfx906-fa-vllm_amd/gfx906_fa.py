@@ -303,10 +303,11 @@ def gather_paged_kv_q8q8(key_cache: torch.Tensor, value_cache: torch.Tensor,
 
 
 def new_workspace(nbytes: int, device) -> torch.Tensor:
-    """Attention workspace: zero-filled once (its per-segment counters must
-    start at 0; every call leaves them at 0).  Reuse it across calls on one
-    stream; calls that overlap on different streams need their own."""
-    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    """Attention workspace (decode plan + partial results of split
+    segments; each call writes what it reads, so no initial contents are
+    needed).  Reuse it across calls on one stream; calls that overlap on
+    different streams need their own."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
 def workspace_size(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int,

@@ -166,12 +166,13 @@ hipError_t gfx906_fa_amd_cache_write_kv(
  *     strides and plane bases 16-byte aligned, max_query_len >= every n_q
  *     (it sizes the prefill grid; max_seq_len is advisory), and a workspace
  *     of at least gfx906_fa_amd_paged_attention_workspace_size(...) bytes,
- *     256-byte aligned and ZERO-FILLED before its first use (it holds
- *     per-(sequence, kv-head) counters that every call returns to zero).
- *     Calls sharing one workspace must be ordered (same stream).
+ *     256-byte aligned (no initial contents needed: each call writes what it
+ *     reads).  Calls sharing one workspace must be ordered (same stream).
  *     Decode-shaped sequences (n_q*Hq/Hkv <= 32 rows) are split stream-K
- *     style: the device's resident waves each stream an equal share of all
- *     their KV sub-pages, merging split segments in the workspace.
+ *     style: the device's resident workgroups each stream an equal,
+ *     contiguous share of all their 16-token KV sub-pages; segments cut
+ *     between workgroups leave partial (m, l, O) in the workspace and a
+ *     second kernel merges them.
  */
 size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int num_tokens,
                                                     int num_heads, int num_kv_heads,

@@ -59,11 +59,11 @@ def test_validation_errors_without_gpu():
 
 def test_workspace_size_plan():
     import gfx906_fa
-    # stream-K decode always needs counters + two partial slots per wave
+    # stream-K decode always needs the plan + two partial slots per workgroup
     a = gfx906_fa.workspace_size(1, 1, 8, 1, 1, 1024)
     b = gfx906_fa.workspace_size(32, 32, 48, 8, 1, 16384)
     assert a > 0 and a % 256 == 0 and b % 256 == 0
-    assert b >= a  # counters grow with num_seqs * Hkv
+    assert b >= a  # the per-sequence prefix grows with num_seqs
     # 30 verify rows (6 q-heads x 5 tokens) use 32-row slots: twice the partials
     assert gfx906_fa.workspace_size(8, 40, 6, 1, 5, 131077) > gfx906_fa.workspace_size(8, 8, 6, 1, 1, 131077)
     # independent of the context length (stream-K shares work per wave)
