@@ -70,15 +70,17 @@ def attention_cpu(query: torch.Tensor, k_aos: torch.Tensor, v_aos: torch.Tensor,
 
 
 def time_cpu_decode(query: torch.Tensor, k_aos, v_aos, block_table, seq_lens, q_lens, scale,
-                    budget_s: float = 15.0):
-    """Times whole sequences in order until `budget_s` is spent (at least one).
-    Returns (seconds, list of sequences timed, threads)."""
+                    budget_s: float = 10.0):
+    """Runs whole sequences in batch order, pass after pass, until `budget_s`
+    is spent (at least one sequence).  Returns (seconds, cached tokens read,
+    sequences run, whole passes, threads)."""
     torch.set_num_threads(torch.get_num_threads())
-    done = []
+    tokens = seqs = 0
     t0 = time.perf_counter()
-    for s in range(len(seq_lens)):
-        attention_cpu(query, k_aos, v_aos, block_table, seq_lens, q_lens, scale, seqs=[s])
-        done.append(s)
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    return time.perf_counter() - t0, done, torch.get_num_threads()
+    while True:
+        for s in range(len(seq_lens)):
+            attention_cpu(query, k_aos, v_aos, block_table, seq_lens, q_lens, scale, seqs=[s])
+            tokens += int(seq_lens[s])
+            seqs += 1
+            if time.perf_counter() - t0 >= budget_s:
+                return time.perf_counter() - t0, tokens, seqs, seqs // len(seq_lens), torch.get_num_threads()

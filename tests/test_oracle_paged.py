@@ -194,3 +194,27 @@ def test_empty_rows_are_zero():
     sl = np.array([0, 16], np.int32)
     a = O.paged_attention_ref(q, kq, vq, bt, sl, qsl, 0.1)
     assert not a[0].any() and a[1].any()
+
+
+def test_cpu_baseline_matches_oracle():
+    """The timed CPU baseline (AoS gather + dequantize + fp32 SDPA) computes
+    the same attention as the oracle, from the planar cache."""
+    from oracle import cpu_baseline as CB
+    rng = np.random.default_rng(8)
+    bs, Hkv, Hq = 16, 2, 8
+    seq_lens, q_lens = [40, 17, 64], [1, 3, 1]
+    bt, nb = O.make_block_table(rng, seq_lens, bs)
+    cache = np.zeros(O.planar_cache_shape(nb, bs, Hkv), np.uint8)
+    k = rng.standard_normal((nb * bs, Hkv, 128)).astype(np.float16)
+    v = rng.standard_normal((nb * bs, Hkv, 128)).astype(np.float16)
+    O.planar_cache_write(k, v, np.arange(nb * bs, dtype=np.int64), cache)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    q = rng.standard_normal((int(qsl[-1]), Hq, 128)).astype(np.float32)
+    ka, va = CB.aos_from_planar(cache)
+    got = CB.attention_cpu(torch.from_numpy(q), ka, va, bt, np.asarray(seq_lens), np.asarray(q_lens), 0.09)
+    kq, vq = O.planar_dequant(cache)
+    exp = O.paged_attention_ref(q, kq, vq, bt, np.asarray(seq_lens, np.int32), qsl, 0.09)
+    assert np.max(np.abs(got.numpy() - exp)) < 1e-4
+    secs, tokens, nseq, passes, thr = CB.time_cpu_decode(torch.from_numpy(q), ka, va, bt, np.asarray(seq_lens),
+                                                         np.asarray(q_lens), 0.09, budget_s=0.05)
+    assert nseq >= 1 and tokens >= 40 and secs > 0
