@@ -27,8 +27,8 @@
 //
 //   attn_decode_kernel   sequences with n_q*G <= 32 rows (decode, verify):
 //                        stream-K over all KV sub-pages, equal share per wave
-//   attn_prefill_kernel  sequences with more rows: each wave owns 32 rows
-//                        and streams their causal KV range
+//   attn_prefill_kernel  sequences with more rows: 128-row workgroups share
+//                        K/V tiles dequantized to fp16 in LDS; 32x32x16 MFMA
 #include <cstdio>
 
 #include "q8_common.h"
@@ -49,8 +49,6 @@ constexpr float LOG2E = 1.4426950408889634f;
 #define GFA_DEC_WPE 3
 #endif
 constexpr int DEC_DEPTH = GFA_DEC_DEPTH;  // decode sub-page ring depth (DEPTH-1 in flight)
-constexpr int PF_NW = 4;                  // prefill waves per workgroup
-constexpr int PF_NRG = 2;                 // prefill 16-row groups per wave
 
 struct AttnParams {
     const void *q;
@@ -598,45 +596,301 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Prefill kernel.  grid (row_tiles, Hkv, num_seqs), block 64*NW; wave w of
-// workgroup x owns rows [64*(NW*x + w), +64) of (seq, kv-head).
-template <int NW, int QDT, int ODT>
-__global__ __launch_bounds__(64 * NW) void attn_prefill_kernel(AttnParams p) {
-    constexpr int NRG = PF_NRG;
-    const int s = blockIdx.z, h = blockIdx.y;
+// Prefill kernel: sequences with more than dec_rows_max packed rows.
+//
+// Workgroup = 4 waves x 32 rows = 128 consecutive packed rows of one
+// (sequence, kv-head).  K/V stream through LDS in 64-key tiles (four 16-token
+// sub-pages; wave w fetches sub-page w), dequantized ONCE per workgroup to
+// fp16 (K^ = q * d_k, V^ = q * d_v, each rounded to fp16) and double
+// buffered, one barrier per tile.  Every wave then runs, per tile,
+//   S^T[64 keys x 32 rows] = K^ . Q^T   16 x v_mfma_f32_32x32x16_f16
+//   O^T[128 d x 32 rows]  += V^T . P^T  16 x v_mfma_f32_32x32x16_f16
+// with Q (pre-scaled by scale*log2 e) held in registers for the whole
+// kernel.  32x32x16 operand layout (lane l, h = l/32): A[i = l%32][k = 8h+e],
+// B[k = 8h+e][j = l%32], D[i = 8(r/4)+4h+r%4][j = l%32] for register r.  A
+// lane's S^T registers 8s..8s+7 are then exactly the keys its P^T operand
+// needs for PV step s when the contraction order inside each 16 keys swaps
+// key bits 2 and 3; V^T is stored in LDS in that order.
+//
+// LDS tile (per stage):
+//   K^   [64 keys][272 B]  (128 fp16 + 16 B pad)
+//   V^T  [128 d][144 B]    (64 fp16 in contraction order + 16 B pad)
+// The pads make every ds_read_b128 of the MFMA operands and every dequant
+// store bank-conflict free with plain (immediate-offset) addressing.
+// Keys at or past the workgroup's kv_end are stored as 0 (their cache bytes
+// may be anything) and masked to -inf in S.
+//
+// grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
+// per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
+// workgroups) and row tiles run last-first, heaviest causal ranges first.
+constexpr int PF_WAVES = 4;
+constexpr int PF_ROWS = 32 * PF_WAVES;
+constexpr int PF_TK = 64;
+constexpr int PF_KPITCH = 272;
+constexpr int PF_VPITCH = 144;
+constexpr int PF_KBYTES = PF_TK * PF_KPITCH;  // 17408
+constexpr int PF_VBYTES = 128 * PF_VPITCH;    // 18432
+constexpr int PF_STAGE = PF_KBYTES + PF_VBYTES;
+
+typedef float float16v_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float16v_t mfma32(half8_t a, half8_t b, float16v_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Raw bytes of one sub-page as a lane of the fetching wave holds them.
+//   K: token t = l%16, group g = l/16: ints of d = 8g+32b+(0..7), b = 0..3
+//      (chunks (4t+g) and 64+(4t+g)), scales of token t (8 B).
+//   V: token quad T = l/16, i = l%16: ints of tokens 4T..4T+3 at
+//      d = i + 16m, m = 0..7 (chunks l and 64+l), scales of tokens 4T..4T+3.
+struct PfRaw {
+    u32x4 kq0, kq1, vq0, vq1, vs0, vs1;
+    u32x2 ks;
+};
+
+__device__ __forceinline__ void pf_fetch(PfRaw &r, const uint8_t *kb, const uint8_t *vb, int lane) {
+    const int t = lane & 15, g = lane >> 4;
+    const u32x4 *k0 = reinterpret_cast<const u32x4 *>(kb + (4 * t + g) * 16);
+    r.kq0 = k0[0];
+    r.kq1 = k0[64];
+    r.ks = *reinterpret_cast<const u32x2 *>(kb + SCALE_OFF + 8 * t);
+    const u32x4 *v0 = reinterpret_cast<const u32x4 *>(vb + lane * 16);
+    r.vq0 = v0[0];
+    r.vq1 = v0[64];
+    const u32x4 *vs = reinterpret_cast<const u32x4 *>(vb + SCALE_OFF + 32 * g);
+    r.vs0 = vs[0];
+    r.vs1 = vs[1];
+}
+
+__device__ __forceinline__ half8_t scale8(half8_t v, half_t s) {
+    const half8_t sv = {s, s, s, s, s, s, s, s};
+    return v * sv;
+}
+
+// Dequantizes the lane's raw sub-page into the LDS stage.  kin = tokens of
+// this sub-page that are valid (0..16); the rest are stored as zeros.
+__device__ __forceinline__ void pf_dequant(PfRaw r, uint8_t *stage, int w, int lane, int kin) {
+    const int t = lane & 15, g = lane >> 4;
+    if (kin < 16) {  // wave-uniform: the tail sub-page of the range
+        if (t >= kin) r.ks = u32x2{0u, 0u};
+        const int T4 = 4 * g;  // V tokens 4T..4T+3 (T = lane/16 = g)
+        const uint32_t m01 = (T4 + 0 < kin ? 0xFFFFu : 0u) | (T4 + 1 < kin ? 0xFFFF0000u : 0u);
+        const uint32_t m23 = (T4 + 2 < kin ? 0xFFFFu : 0u) | (T4 + 3 < kin ? 0xFFFF0000u : 0u);
+        r.vs0 &= u32x4{m01, m23, m01, m23};
+        r.vs1 &= u32x4{m01, m23, m01, m23};
+    }
+    // K^: row 16w + t, d chunks 4b + g (8 fp16 each)
+    uint8_t *krow = stage + (16 * w + t) * PF_KPITCH + 16 * g;
+    // (vector elements are copied to scalars before __builtin_bit_cast: a
+    // bit_cast of an ext_vector element lvalue reads element 0 with this clang)
+    const uint32_t ksw0 = r.ks[0], ksw1 = r.ks[1];
+    const half2_t ks01 = __builtin_bit_cast(half2_t, ksw0);
+    const half2_t ks23 = __builtin_bit_cast(half2_t, ksw1);
+    *reinterpret_cast<half8_t *>(krow + 0 * 64) = scale8(i8x8_to_half8(r.kq0[0], r.kq0[1]), ks01[0]);
+    *reinterpret_cast<half8_t *>(krow + 1 * 64) = scale8(i8x8_to_half8(r.kq0[2], r.kq0[3]), ks01[1]);
+    *reinterpret_cast<half8_t *>(krow + 2 * 64) = scale8(i8x8_to_half8(r.kq1[0], r.kq1[1]), ks23[0]);
+    *reinterpret_cast<half8_t *>(krow + 3 * 64) = scale8(i8x8_to_half8(r.kq1[2], r.kq1[3]), ks23[1]);
+    // V^T: rows d = i + 16m; the 4 tokens 4T..4T+3 of sub-page w sit at
+    // contraction position 16w + 8(T&1) + 4(T>>1) (key bits 2 and 3 swapped)
+    const int i = lane & 15, T = lane >> 4;
+    uint8_t *vcol = stage + PF_KBYTES + i * PF_VPITCH + 2 * (16 * w + 8 * (T & 1) + 4 * (T >> 1));
+    const uint32_t vsw[8] = {r.vs0[0], r.vs0[1], r.vs0[2], r.vs0[3], r.vs1[0], r.vs1[1], r.vs1[2], r.vs1[3]};
+    const uint32_t vqw[8] = {r.vq0[0], r.vq0[1], r.vq0[2], r.vq0[3], r.vq1[0], r.vq1[1], r.vq1[2], r.vq1[3]};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const uint32_t q = vqw[m];
+        const int b = m >> 1;  // d = i + 16m lies in block m/2: scale dwords 2b, 2b+1
+        const half2_t s01 = __builtin_bit_cast(half2_t, vsw[2 * b]);
+        const half2_t s23 = __builtin_bit_cast(half2_t, vsw[2 * b + 1]);
+        half2_t lo, hi;
+        i8x4_to_f16x4(q, lo, hi);
+        lo *= s01;
+        hi *= s23;
+        *reinterpret_cast<half4_t *>(vcol + 16 * m * PF_VPITCH) = half4_t{lo[0], lo[1], hi[0], hi[1]};
+    }
+}
+
+template <int QDT, int ODT>
+__global__ __launch_bounds__(64 * PF_WAVES)
+__attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * PF_STAGE];
+    const int s = blockIdx.y;
+    const int Hkv = p.Hkv;
+    const int h = blockIdx.x % Hkv;
+    const int rt = (gridDim.x / Hkv) - 1 - (int)(blockIdx.x / Hkv);
     const int q0 = p.qsl[s];
     const int nq = p.qsl[s + 1] - q0;
     const int nrows = nq * p.G;
-    if (nq <= 0 || nrows <= p.dec_rows_max) return;
+    if (nq <= 0 || nrows <= p.dec_rows_max) return;  // uniform over the workgroup
+    const int row0 = PF_ROWS * rt;
+    if (row0 >= nrows) return;
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int row0 = 16 * NRG * (NW * blockIdx.x + w);
-    if (row0 >= nrows) return;  // whole wave; no barriers in this kernel
-    const int i16 = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hb = lane >> 5;
     const int sl = p.seq_lens[s];
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int jlast = (min(row0 + 16 * NRG, nrows) - 1) / p.G;
+    const int jlast = (min(row0 + PF_ROWS, nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
+    const int ntk = (kv_end + PF_TK - 1) / PF_TK;
 
-    half8_t qf[NRG][4];
-    int lim[NRG];
-    load_rows<NRG, QDT>(p, h, q0, nrows, row0, sl, qa, i16, g, qf, lim);
-    WaveAcc<NRG> acc;
-    acc_init(acc);
-    stream_range<NRG, false, 2>(acc, p, s, h, 0, kv_end, qf, lim, lane, i16, g);
+    // this lane's query row, its causal bound and its Q^T fragments
+    const int r = row0 + 32 * w + (lane & 31);
+    const bool rvalid = r < nrows;
+    const int j = rvalid ? r / p.G : 0;
+    const int hq = h * p.G + (rvalid ? r - j * p.G : 0);
+    const int lim = rvalid ? (p.causal ? min(sl - 1, qa + j) : sl - 1) : INT32_MAX;
+    half8_t qf[8];
+    {
+        const float c = p.scale_log2e;
+        const int64_t qoff = (int64_t)(q0 + j) * p.q_ts + (int64_t)hq * p.q_hs + 8 * hb;
 #pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) {
-        const float l = xrow_sum(acc.l[rg]);
-        const int r = row0 + 16 * rg + i16;
-        if (r >= nrows) continue;
-        const int j = r / p.G;
-        const int hq = h * p.G + (r - j * p.G);
-        const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs;
-        const float inv = l > 0.f ? 1.0f / l : 0.0f;
+        for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
-        for (int mm = 0; mm < 8; ++mm)
+            for (int e = 0; e < 8; ++e)
+                qf[kk][e] = rvalid ? (half_t)(load_as_f32<QDT>(p.q, qoff + 16 * kk + e) * c) : (half_t)0.0f;
+        }
+    }
+    int lim_min;  // smallest bound over the wave's rows: tiles below it need no mask
+    {
+        const float f = (float)min(lim, 1 << 24);
+        lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
+    }
+
+    // per-wave page ids: lane i holds the page of this wave's sub-page in
+    // tile 64*chunk + i
+    const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
+    const int bs = p.block_size;
+    const int last_sp = (kv_end - 1) >> 4;  // last sub-page with a valid key
+    auto sp_of = [&](int kt) { return min(4 * kt + w, last_sp); };
+    auto load_pg = [&](int chunk) -> int {
+        const int kt = 64 * chunk + lane;
+        return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
+    };
+    const uint8_t *kbase = p.kc + (int64_t)h * p.chs;
+    const uint8_t *vbase = p.vc + (int64_t)h * p.chs;
+    int pg_cur = 0, pg_nxt = 0, chunk = 0;
+    auto fetch = [&](PfRaw &raw, int kt) {
+        if ((kt >> 6) != chunk) {  // uniform
+            chunk = kt >> 6;
+            pg_cur = pg_nxt;
+            pg_nxt = 64 * (chunk + 1) < ntk ? load_pg(chunk + 1) : 0;
+        }
+        const int sp = sp_of(kt);
+        const int64_t page = __builtin_amdgcn_readlane(pg_cur, kt & 63);
+        const int64_t off = page * p.cbs + (int64_t)(((16 * sp) % bs) >> 4) * SUBPAGE_BYTES;
+        pf_fetch(raw, kbase + off, vbase + off, lane);
+    };
+    auto kin_of = [&](int kt) {  // valid tokens of this wave's sub-page of tile kt
+        const int k0 = 64 * kt + 16 * w;
+        return max(0, min(16, kv_end - k0));
+    };
+
+    float16v_t o[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + 16 * mm + 4 * g + i, acc.o[rg][mm][i] * inv);
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    PfRaw raw;
+    if (ntk > 0) {
+        pg_cur = load_pg(0);
+        pg_nxt = ntk > 64 ? load_pg(1) : 0;
+        fetch(raw, 0);
+        pf_dequant(raw, lds, w, lane, kin_of(0));
+    }
+    __syncthreads();
+
+    // lane-constant LDS offsets of the MFMA operands
+    const int kread = (lane & 31) * PF_KPITCH + 16 * hb;            // + 32*st*KPITCH + 32*kk
+    const int vread = PF_KBYTES + (lane & 31) * PF_VPITCH + 16 * hb;  // + 32*dt*VPITCH + 16*(4st+2sg)
+
+    for (int kt = 0; kt < ntk; ++kt) {
+        uint8_t *stage = lds + (kt & 1) * PF_STAGE;
+        const bool more = kt + 1 < ntk;
+        if (more) fetch(raw, kt + 1);
+
+        // S^T = K^ . Q^T for the two 32-key halves of the tile
+        float16v_t sacc[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sacc[st][e] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const half8_t a = *reinterpret_cast<const half8_t *>(stage + kread + 32 * st * PF_KPITCH + 32 * kk);
+                sacc[st] = mfma32(a, qf[kk], sacc[st]);
+            }
+        }
+        const int kbase_t = PF_TK * kt;
+        if (kbase_t + PF_TK - 1 > lim_min) {  // uniform: tile crosses some row's bound
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = kbase_t + 32 * st + 8 * (e >> 2) + 4 * hb + (e & 3);
+                    sacc[st][e] = key <= lim ? sacc[st][e] : -INFINITY;
+                }
+        }
+        float mx = sacc[0][0];
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const bool need = mx > m_run + LAZY_TAU;
+        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after the first tile
+            const float mn = need ? mx : m_run;
+            const float alpha = need ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
+            m_run = mn;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        }
+        const float nms = m_run == -INFINITY ? 0.0f : -m_run;
+        const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+#pragma unroll
+            for (int sg = 0; sg < 2; ++sg) {
+                half8_t pb;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + e] + nms);
+                    const float p1 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + e + 1] + nms);
+                    const half2_t pp = {(half_t)p0, (half_t)p1};
+                    l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
+                    pb[e] = pp[0];
+                    pb[e + 1] = pp[1];
+                }
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const half8_t a = *reinterpret_cast<const half8_t *>(
+                        stage + vread + 32 * dt * PF_VPITCH + 16 * (4 * st + 2 * sg));
+                    o[dt] = mfma32(a, pb, o[dt]);
+                }
+            }
+        }
+        if (more) pf_dequant(raw, lds + ((kt + 1) & 1) * PF_STAGE, w, lane, kin_of(kt + 1));
+        __syncthreads();
+    }
+
+    // normalise and store: register e of d-tile dt is d = 32dt + 8(e/4) + 4hb + e%4
+    {
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+        const float l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        if (rvalid) {
+            const float inv = l > 0.f ? 1.0f / l : 0.0f;
+            const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + 4 * hb;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    store_out<ODT>(p.out, ob + 32 * dt + 8 * (e >> 2) + (e & 3), o[dt][e] * inv);
+        }
     }
 }
 
@@ -697,8 +951,8 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
-        const int tiles = (rows + 16 * PF_NRG * PF_NW - 1) / (16 * PF_NRG * PF_NW);
-        attn_prefill_kernel<PF_NW, QDT, ODT><<<dim3(tiles, num_kv_heads, num_seqs), 64 * PF_NW, 0, stream>>>(p);
+        const int tiles = (rows + PF_ROWS - 1) / PF_ROWS;
+        attn_prefill_kernel<QDT, ODT><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
     }
     return hipGetLastError();
 }
