@@ -30,6 +30,7 @@
 //   attn_prefill_kernel  sequences with more rows: 128-row workgroups share
 //                        K/V tiles dequantized to fp16 in LDS; 32x32x16 MFMA
 #include <cstdio>
+#include <type_traits>
 
 #include "q8_common.h"
 
@@ -598,32 +599,40 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // ---------------------------------------------------------------------------
 // Prefill kernel: sequences with more than dec_rows_max packed rows.
 //
-// Workgroup = 4 waves x 32 rows = 128 consecutive packed rows of one
+// Workgroup = 8 waves x 32 rows = 256 consecutive packed rows of one
 // (sequence, kv-head).  K/V stream through LDS in 64-key tiles (four 16-token
-// sub-pages; wave w fetches sub-page w), dequantized ONCE per workgroup to
-// fp16 (K^ = q * d_k, V^ = q * d_v, each rounded to fp16) and double
-// buffered, one barrier per tile.  Every wave then runs, per tile,
-//   S^T[64 keys x 32 rows] = K^ . Q^T   16 x v_mfma_f32_32x32x16_f16
-//   O^T[128 d x 32 rows]  += V^T . P^T  16 x v_mfma_f32_32x32x16_f16
+// sub-pages), dequantized ONCE per workgroup to fp16 (K^ = q * d_k,
+// V^ = q * d_v, each rounded to fp16): wave w fetches and dequantizes half
+// w/4 (two Q8_0 blocks) of the K and V of sub-page w%4.  Every wave runs, per
+// tile,
+//   S'^T[64 keys x 32 rows] = K^ . Q^T - m   16 x v_mfma_f32_32x32x16_f16
+//   O^T[128 d x 32 rows]   += V^T . P^T      16 x v_mfma_f32_32x32x16_f16
 // with Q (pre-scaled by scale*log2 e) held in registers for the whole
-// kernel.  32x32x16 operand layout (lane l, h = l/32): A[i = l%32][k = 8h+e],
+// kernel and the running row max m fed in as the accumulator input.
+// 32x32x16 operand layout (lane l, h = l/32): A[i = l%32][k = 8h+e],
 // B[k = 8h+e][j = l%32], D[i = 8(r/4)+4h+r%4][j = l%32] for register r.  A
 // lane's S^T registers 8s..8s+7 are then exactly the keys its P^T operand
 // needs for PV step s when the contraction order inside each 16 keys swaps
 // key bits 2 and 3; V^T is stored in LDS in that order.
+//
+// Software pipeline, one barrier per tile: iteration kt issues the HBM loads
+// of tile kt+2, dequantizes tile kt+1 (loaded one iteration earlier) into
+// the other LDS stage while the QK MFMAs of tile kt run, then the softmax
+// of tile kt overlaps its PV MFMAs.
 //
 // LDS tile (per stage):
 //   K^   [64 keys][272 B]  (128 fp16 + 16 B pad)
 //   V^T  [128 d][144 B]    (64 fp16 in contraction order + 16 B pad)
 // The pads make every ds_read_b128 of the MFMA operands and every dequant
 // store bank-conflict free with plain (immediate-offset) addressing.
-// Keys at or past the workgroup's kv_end are stored as 0 (their cache bytes
-// may be anything) and masked to -inf in S.
+// Keys at or past the workgroup's kv_end are masked to -inf in S; the V
+// scales are made finite during dequantization so their P = 0 products stay
+// 0 whatever those cache bytes hold.
 //
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
-constexpr int PF_WAVES = 4;
+constexpr int PF_WAVES = 8;
 constexpr int PF_ROWS = 32 * PF_WAVES;
 constexpr int PF_TK = 64;
 constexpr int PF_KPITCH = 272;
@@ -633,33 +642,31 @@ constexpr int PF_VBYTES = 128 * PF_VPITCH;    // 18432
 constexpr int PF_STAGE = PF_KBYTES + PF_VBYTES;
 
 typedef float float16v_t __attribute__((ext_vector_type(16)));
+struct PHalf8 {
+    half2_t h[4];
+};
 
 __device__ __forceinline__ float16v_t mfma32(half8_t a, half8_t b, float16v_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Raw bytes of one sub-page as a lane of the fetching wave holds them.
-//   K: token t = l%16, group g = l/16: ints of d = 8g+32b+(0..7), b = 0..3
-//      (chunks (4t+g) and 64+(4t+g)), scales of token t (8 B).
-//   V: token quad T = l/16, i = l%16: ints of tokens 4T..4T+3 at
-//      d = i + 16m, m = 0..7 (chunks l and 64+l), scales of tokens 4T..4T+3.
+// Raw bytes of one half (hf = 0, 1) of a sub-page as a lane holds them:
+// the Q8_0 blocks 2hf and 2hf+1 of K and of V.
+//   K: token t = l%16, group g = l/16: k = ints of d = 8g + 32b + (0..7),
+//      b = 2hf, 2hf+1 (chunk hf*64 + 4t+g); ks = the two scales (t, b).
+//   V: token quad T = l/16, i = l%16: v = ints of tokens 4T..4T+3 at
+//      d = i + 16m, m = 4hf..4hf+3 (chunk hf*64 + l); vs = their scales.
 struct PfRaw {
-    u32x4 kq0, kq1, vq0, vq1, vs0, vs1;
-    u32x2 ks;
+    u32x4 k, v, vs;
+    uint32_t ks;
 };
 
-__device__ __forceinline__ void pf_fetch(PfRaw &r, const uint8_t *kb, const uint8_t *vb, int lane) {
+__device__ __forceinline__ void pf_fetch(PfRaw &r, const uint8_t *kb, const uint8_t *vb, int lane, int hf) {
     const int t = lane & 15, g = lane >> 4;
-    const u32x4 *k0 = reinterpret_cast<const u32x4 *>(kb + (4 * t + g) * 16);
-    r.kq0 = k0[0];
-    r.kq1 = k0[64];
-    r.ks = *reinterpret_cast<const u32x2 *>(kb + SCALE_OFF + 8 * t);
-    const u32x4 *v0 = reinterpret_cast<const u32x4 *>(vb + lane * 16);
-    r.vq0 = v0[0];
-    r.vq1 = v0[64];
-    const u32x4 *vs = reinterpret_cast<const u32x4 *>(vb + SCALE_OFF + 32 * g);
-    r.vs0 = vs[0];
-    r.vs1 = vs[1];
+    r.k = *reinterpret_cast<const u32x4 *>(kb + hf * 1024 + (4 * t + g) * 16);
+    r.ks = *reinterpret_cast<const uint32_t *>(kb + SCALE_OFF + 8 * t + 4 * hf);
+    r.v = *reinterpret_cast<const u32x4 *>(vb + hf * 1024 + lane * 16);
+    r.vs = *reinterpret_cast<const u32x4 *>(vb + SCALE_OFF + 32 * g + 16 * hf);
 }
 
 __device__ __forceinline__ half8_t scale8(half8_t v, half_t s) {
@@ -667,46 +674,48 @@ __device__ __forceinline__ half8_t scale8(half8_t v, half_t s) {
     return v * sv;
 }
 
-// Dequantizes the lane's raw sub-page into the LDS stage.  kin = tokens of
-// this sub-page that are valid (0..16); the rest are stored as zeros.
-__device__ __forceinline__ void pf_dequant(PfRaw r, uint8_t *stage, int w, int lane, int kin) {
-    const int t = lane & 15, g = lane >> 4;
-    if (kin < 16) {  // wave-uniform: the tail sub-page of the range
-        if (t >= kin) r.ks = u32x2{0u, 0u};
-        const int T4 = 4 * g;  // V tokens 4T..4T+3 (T = lane/16 = g)
-        const uint32_t m01 = (T4 + 0 < kin ? 0xFFFFu : 0u) | (T4 + 1 < kin ? 0xFFFF0000u : 0u);
-        const uint32_t m23 = (T4 + 2 < kin ? 0xFFFFu : 0u) | (T4 + 3 < kin ? 0xFFFF0000u : 0u);
-        r.vs0 &= u32x4{m01, m23, m01, m23};
-        r.vs1 &= u32x4{m01, m23, m01, m23};
+// fp16 pair with Inf / NaN replaced by +-65504 (v_pk_max/min_f16 return the
+// non-NaN operand).
+__device__ __forceinline__ half2_t finite2(half2_t x) {
+    const half2_t hi = {(half_t)65504.0f, (half_t)65504.0f};
+    return __builtin_elementwise_min(__builtin_elementwise_max(x, -hi), hi);
+}
+
+// Dequantizes the lane's raw half sub-page into the LDS stage (sub-page sp of
+// the tile).  Bytes of tokens past the valid range are dequantized as they
+// are: their scores are masked to -inf (P = 0) and the V scales are made
+// finite here, so 0 * V^ stays 0.
+__device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int sp, int lane, int hf) {
+    {
+        const int t = lane & 15, g = lane >> 4;
+        // (vector elements are copied to scalars before __builtin_bit_cast: a
+        // bit_cast of an ext_vector element lvalue reads element 0 with this clang)
+        const half2_t ks = __builtin_bit_cast(half2_t, r.ks);
+        const uint32_t k0 = r.k[0], k1 = r.k[1], k2 = r.k[2], k3 = r.k[3];
+        // K^: row 16sp + t, d chunks 4b + g (8 fp16 each)
+        uint8_t *krow = stage + (16 * sp + t) * PF_KPITCH + 16 * g + 128 * hf;
+        *reinterpret_cast<half8_t *>(krow) = scale8(i8x8_to_half8(k0, k1), ks[0]);
+        *reinterpret_cast<half8_t *>(krow + 64) = scale8(i8x8_to_half8(k2, k3), ks[1]);
     }
-    // K^: row 16w + t, d chunks 4b + g (8 fp16 each)
-    uint8_t *krow = stage + (16 * w + t) * PF_KPITCH + 16 * g;
-    // (vector elements are copied to scalars before __builtin_bit_cast: a
-    // bit_cast of an ext_vector element lvalue reads element 0 with this clang)
-    const uint32_t ksw0 = r.ks[0], ksw1 = r.ks[1];
-    const half2_t ks01 = __builtin_bit_cast(half2_t, ksw0);
-    const half2_t ks23 = __builtin_bit_cast(half2_t, ksw1);
-    *reinterpret_cast<half8_t *>(krow + 0 * 64) = scale8(i8x8_to_half8(r.kq0[0], r.kq0[1]), ks01[0]);
-    *reinterpret_cast<half8_t *>(krow + 1 * 64) = scale8(i8x8_to_half8(r.kq0[2], r.kq0[3]), ks01[1]);
-    *reinterpret_cast<half8_t *>(krow + 2 * 64) = scale8(i8x8_to_half8(r.kq1[0], r.kq1[1]), ks23[0]);
-    *reinterpret_cast<half8_t *>(krow + 3 * 64) = scale8(i8x8_to_half8(r.kq1[2], r.kq1[3]), ks23[1]);
-    // V^T: rows d = i + 16m; the 4 tokens 4T..4T+3 of sub-page w sit at
-    // contraction position 16w + 8(T&1) + 4(T>>1) (key bits 2 and 3 swapped)
-    const int i = lane & 15, T = lane >> 4;
-    uint8_t *vcol = stage + PF_KBYTES + i * PF_VPITCH + 2 * (16 * w + 8 * (T & 1) + 4 * (T >> 1));
-    const uint32_t vsw[8] = {r.vs0[0], r.vs0[1], r.vs0[2], r.vs0[3], r.vs1[0], r.vs1[1], r.vs1[2], r.vs1[3]};
-    const uint32_t vqw[8] = {r.vq0[0], r.vq0[1], r.vq0[2], r.vq0[3], r.vq1[0], r.vq1[1], r.vq1[2], r.vq1[3]};
+    {
+        const int i = lane & 15, T = lane >> 4;
+        const uint32_t vq[4] = {r.v[0], r.v[1], r.v[2], r.v[3]};
+        const uint32_t vsw[4] = {r.vs[0], r.vs[1], r.vs[2], r.vs[3]};
+        // V^T: rows d = i + 16m; the 4 tokens 4T..4T+3 of sub-page sp sit at
+        // contraction position 16sp + 8(T&1) + 4(T>>1) (key bits 2 and 3 swapped)
+        uint8_t *vcol = stage + PF_KBYTES + (i + 64 * hf) * PF_VPITCH +
+                        2 * (16 * sp + 8 * (T & 1) + 4 * (T >> 1));
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const uint32_t q = vqw[m];
-        const int b = m >> 1;  // d = i + 16m lies in block m/2: scale dwords 2b, 2b+1
-        const half2_t s01 = __builtin_bit_cast(half2_t, vsw[2 * b]);
-        const half2_t s23 = __builtin_bit_cast(half2_t, vsw[2 * b + 1]);
-        half2_t lo, hi;
-        i8x4_to_f16x4(q, lo, hi);
-        lo *= s01;
-        hi *= s23;
-        *reinterpret_cast<half4_t *>(vcol + 16 * m * PF_VPITCH) = half4_t{lo[0], lo[1], hi[0], hi[1]};
+        for (int mm = 0; mm < 4; ++mm) {
+            const int b = mm >> 1;  // block 2hf + b: scale dwords 2b (tokens 0,1), 2b+1 (2,3)
+            const half2_t s01 = finite2(__builtin_bit_cast(half2_t, vsw[2 * b]));
+            const half2_t s23 = finite2(__builtin_bit_cast(half2_t, vsw[2 * b + 1]));
+            half2_t lo, hi;
+            i8x4_to_f16x4(vq[mm], lo, hi);
+            lo *= s01;
+            hi *= s23;
+            *reinterpret_cast<half4_t *>(vcol + 16 * mm * PF_VPITCH) = half4_t{lo[0], lo[1], hi[0], hi[1]};
+        }
     }
 }
 
@@ -756,33 +765,30 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
     }
 
-    // per-wave page ids: lane i holds the page of this wave's sub-page in
-    // tile 64*chunk + i
+    // Wave w fetches and dequantizes half hf = w/4 of sub-page w%4 of every
+    // tile (K and V).  Page ids come from two lane-distributed windows of 64
+    // tiles (lane i of pw0 / pw1: the page of this wave's sub-page in tile
+    // cbase + i / cbase + 64 + i); tiles past the range read page 0 (their
+    // bytes land in an LDS stage that is never read).
     const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
     const int bs = p.block_size;
-    const int last_sp = (kv_end - 1) >> 4;  // last sub-page with a valid key
-    auto sp_of = [&](int kt) { return min(4 * kt + w, last_sp); };
-    auto load_pg = [&](int chunk) -> int {
-        const int kt = 64 * chunk + lane;
+    const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
+    const int wsp = w & 3, hf = w >> 2;
+    auto sp_of = [&](int kt) { return min(4 * kt + wsp, last_sp); };
+    auto load_pg = [&](int c) -> int {
+        const int kt = 64 * c + lane;
         return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
     };
-    const uint8_t *kbase = p.kc + (int64_t)h * p.chs;
-    const uint8_t *vbase = p.vc + (int64_t)h * p.chs;
-    int pg_cur = 0, pg_nxt = 0, chunk = 0;
-    auto fetch = [&](PfRaw &raw, int kt) {
-        if ((kt >> 6) != chunk) {  // uniform
-            chunk = kt >> 6;
-            pg_cur = pg_nxt;
-            pg_nxt = 64 * (chunk + 1) < ntk ? load_pg(chunk + 1) : 0;
-        }
-        const int sp = sp_of(kt);
-        const int64_t page = __builtin_amdgcn_readlane(pg_cur, kt & 63);
-        const int64_t off = page * p.cbs + (int64_t)(((16 * sp) % bs) >> 4) * SUBPAGE_BYTES;
-        pf_fetch(raw, kbase + off, vbase + off, lane);
-    };
-    auto kin_of = [&](int kt) {  // valid tokens of this wave's sub-page of tile kt
-        const int k0 = 64 * kt + 16 * w;
-        return max(0, min(16, kv_end - k0));
+    const uint8_t *kplane = p.kc + (int64_t)h * p.chs;
+    const uint8_t *vplane = p.vc + (int64_t)h * p.chs;
+    int pw0 = 0, pw1 = 0, cbase = 0;
+    auto fetch = [&](PfRaw &rw, int kt) {
+        const int rel = kt - cbase;  // 0..127, uniform
+        const int pa = __builtin_amdgcn_readlane(pw0, rel & 63);
+        const int pb = __builtin_amdgcn_readlane(pw1, rel & 63);
+        const int64_t page = rel < 64 ? pa : pb;
+        const int64_t off = page * p.cbs + (int64_t)(((16 * sp_of(kt)) % bs) >> 4) * SUBPAGE_BYTES;
+        pf_fetch(rw, kplane + off, vplane + off, lane, hf);
     };
 
     float16v_t o[4];
@@ -790,32 +796,31 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    PfRaw raw;
-    if (ntk > 0) {
-        pg_cur = load_pg(0);
-        pg_nxt = ntk > 64 ? load_pg(1) : 0;
-        fetch(raw, 0);
-        pf_dequant(raw, lds, w, lane, kin_of(0));
-    }
-    __syncthreads();
+    // Running max m (log2 units) enters the S MFMA chain as its accumulator
+    // input (-m in all 16 lanes of cneg), so S' = S - m comes out of the
+    // matrix core directly.  has_m: a visible key has been seen (m valid).
+    float m_use = 0.0f, l_run = 0.0f;
+    bool has_m = false;
+    float16v_t cneg;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) cneg[e] = 0.0f;
 
     // lane-constant LDS offsets of the MFMA operands
     const int kread = (lane & 31) * PF_KPITCH + 16 * hb;            // + 32*st*KPITCH + 32*kk
     const int vread = PF_KBYTES + (lane & 31) * PF_VPITCH + 16 * hb;  // + 32*dt*VPITCH + 16*(4st+2sg)
 
-    for (int kt = 0; kt < ntk; ++kt) {
-        uint8_t *stage = lds + (kt & 1) * PF_STAGE;
-        const bool more = kt + 1 < ntk;
-        if (more) fetch(raw, kt + 1);
+    // One pipeline step: loads of tile kt+2 into rf, dequant of tile kt+1
+    // from rd, attention over tile kt.
+    auto step = [&](int kt, PfRaw &rf, const PfRaw &rd) {
+        const uint8_t *stage = lds + (kt & 1) * PF_STAGE;
+        fetch(rf, kt + 2);
+        pf_dequant(rd, lds + ((kt + 1) & 1) * PF_STAGE, wsp, lane, hf);
 
-        // S^T = K^ . Q^T for the two 32-key halves of the tile
+        // S'^T = K^ . Q^T - m for the two 32-key halves of the tile
         float16v_t sacc[2];
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) sacc[st][e] = 0.0f;
+            sacc[st] = cneg;
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
                 const half8_t a = *reinterpret_cast<const half8_t *>(stage + kread + 32 * st * PF_KPITCH + 32 * kk);
@@ -841,31 +846,36 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
             mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
         }
-        const bool need = mx > m_run + LAZY_TAU;
+        // lazy rescale: move m only when the tile max exceeds it by > LAZY_TAU
+        // (or on the first visible key of the row)
+        const bool need = has_m ? mx > LAZY_TAU : mx > -INFINITY;
         if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after the first tile
-            const float mn = need ? mx : m_run;
-            const float alpha = need ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
-            m_run = mn;
+            const float delta = need ? mx : 0.0f;
+            const float alpha = (need && has_m) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+            m_use += delta;
+            has_m = has_m || need;
             l_run *= alpha;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) sacc[st] -= delta;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) cneg[e] = -m_use;
         }
-        const float nms = m_run == -INFINITY ? 0.0f : -m_run;
         const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
 #pragma unroll
             for (int sg = 0; sg < 2; ++sg) {
-                half8_t pb;
+                PHalf8 pk;
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const float p0 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + e] + nms);
-                    const float p1 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + e + 1] + nms);
-                    const half2_t pp = {(half_t)p0, (half_t)p1};
-                    l_run = __builtin_amdgcn_fdot2(pp, ones, l_run, false);
-                    pb[e] = pp[0];
-                    pb[e + 1] = pp[1];
+                for (int e = 0; e < 4; ++e) {
+                    const float p0 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + 2 * e]);
+                    const float p1 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + 2 * e + 1]);
+                    pk.h[e] = half2_t{(half_t)p0, (half_t)p1};
+                    l_run = __builtin_amdgcn_fdot2(pk.h[e], ones, l_run, false);
                 }
+                const half8_t pb = __builtin_bit_cast(half8_t, pk);
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) {
                     const half8_t a = *reinterpret_cast<const half8_t *>(
@@ -874,8 +884,26 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 }
             }
         }
-        if (more) pf_dequant(raw, lds + ((kt + 1) & 1) * PF_STAGE, w, lane, kin_of(kt + 1));
         __syncthreads();
+    };
+    PfRaw r0, r1;
+    if (ntk > 0) {
+        pw0 = load_pg(0);
+        pw1 = ntk > 64 ? load_pg(1) : 0;
+        fetch(r0, 0);
+        fetch(r1, 1);
+        pf_dequant(r0, lds, wsp, lane, hf);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ntk; kt += 2) {
+        // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2
+        step(kt, r0, r1);
+        if (kt + 1 < ntk) step(kt + 1, r1, r0);  // uniform
+        if (kt + 2 - cbase >= 64) {             // slide the page windows (uniform)
+            cbase += 64;
+            pw0 = pw1;
+            pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
+        }
     }
 
     // normalise and store: register e of d-tile dt is d = 32dt + 8(e/4) + 4hb + e%4
@@ -951,7 +979,7 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
-        const int tiles = (rows + PF_ROWS - 1) / PF_ROWS;
+        const int tiles = (rows + 32 * PF_WAVES - 1) / (32 * PF_WAVES);
         attn_prefill_kernel<QDT, ODT><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
     }
     return hipGetLastError();
