@@ -632,13 +632,21 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
+#ifndef GFA_PF_SCHED
+#define GFA_PF_SCHED 0  // VALU instructions per QK MFMA slot (0: compiler's schedule)
+#endif
 constexpr int PF_WAVES = 8;
 constexpr int PF_ROWS = 32 * PF_WAVES;
-constexpr int PF_TK = 64;
+#ifndef GFA_PF_TK
+#define GFA_PF_TK 64
+#endif
+constexpr int PF_TK = GFA_PF_TK;              // keys per LDS tile: 64 or 128
+constexpr int PF_NSP = PF_TK / 16;            // sub-pages per tile
+constexpr int PF_NST = PF_TK / 32;            // 32-key S subtiles per tile
 constexpr int PF_KPITCH = 272;
-constexpr int PF_VPITCH = 144;
-constexpr int PF_KBYTES = PF_TK * PF_KPITCH;  // 17408
-constexpr int PF_VBYTES = 128 * PF_VPITCH;    // 18432
+constexpr int PF_VPITCH = 2 * PF_TK + 16;
+constexpr int PF_KBYTES = PF_TK * PF_KPITCH;
+constexpr int PF_VBYTES = 128 * PF_VPITCH;
 constexpr int PF_STAGE = PF_KBYTES + PF_VBYTES;
 
 typedef float float16v_t __attribute__((ext_vector_type(16)));
@@ -682,9 +690,11 @@ __device__ __forceinline__ half2_t finite2(half2_t x) {
 }
 
 // Dequantizes the lane's raw half sub-page into the LDS stage (sub-page sp of
-// the tile).  Bytes of tokens past the valid range are dequantized as they
-// are: their scores are masked to -inf (P = 0) and the V scales are made
-// finite here, so 0 * V^ stays 0.
+// the tile).  TAIL (the last tile of the range, the only one that can hold
+// keys past kv_end): bytes of tokens past the valid range are dequantized as
+// they are - their scores are masked to -inf (P = 0) - and the V scales are
+// made finite so that 0 * V^ stays 0.
+template <bool TAIL>
 __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int sp, int lane, int hf) {
     {
         const int t = lane & 15, g = lane >> 4;
@@ -708,8 +718,12 @@ __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int s
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) {
             const int b = mm >> 1;  // block 2hf + b: scale dwords 2b (tokens 0,1), 2b+1 (2,3)
-            const half2_t s01 = finite2(__builtin_bit_cast(half2_t, vsw[2 * b]));
-            const half2_t s23 = finite2(__builtin_bit_cast(half2_t, vsw[2 * b + 1]));
+            half2_t s01 = __builtin_bit_cast(half2_t, vsw[2 * b]);
+            half2_t s23 = __builtin_bit_cast(half2_t, vsw[2 * b + 1]);
+            if (TAIL) {
+                s01 = finite2(s01);
+                s23 = finite2(s23);
+            }
             half2_t lo, hi;
             i8x4_to_f16x4(vq[mm], lo, hi);
             lo *= s01;
@@ -722,7 +736,11 @@ __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int s
 template <int QDT, int ODT>
 __global__ __launch_bounds__(64 * PF_WAVES)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * PF_STAGE];
+    // two LDS stages as distinct objects: the compiler can then prove that
+    // the dequant stores (one stage) and the MFMA operand reads (the other)
+    // are independent and interleave them
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[PF_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[PF_STAGE];
     const int s = blockIdx.y;
     const int Hkv = p.Hkv;
     const int h = blockIdx.x % Hkv;
@@ -773,8 +791,11 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
     const int bs = p.block_size;
     const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
-    const int wsp = w & 3, hf = w >> 2;
-    auto sp_of = [&](int kt) { return min(4 * kt + wsp, last_sp); };
+    // 64-key tiles: wave w takes half w/4 of sub-page w%4; 128-key tiles:
+    // wave w takes both halves of sub-page w
+    const int wsp = PF_NSP == 4 ? (w & 3) : w;
+    const int hf = PF_NSP == 4 ? (w >> 2) : 0;
+    auto sp_of = [&](int kt) { return min(PF_NSP * kt + wsp, last_sp); };
     auto load_pg = [&](int c) -> int {
         const int kt = 64 * c + lane;
         return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
@@ -782,13 +803,22 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     const uint8_t *kplane = p.kc + (int64_t)h * p.chs;
     const uint8_t *vplane = p.vc + (int64_t)h * p.chs;
     int pw0 = 0, pw1 = 0, cbase = 0;
-    auto fetch = [&](PfRaw &rw, int kt) {
+    struct PfRawT {
+        PfRaw h[PF_NSP == 8 ? 2 : 1];
+    };
+    auto fetch = [&](PfRawT &rw, int kt) {
         const int rel = kt - cbase;  // 0..127, uniform
         const int pa = __builtin_amdgcn_readlane(pw0, rel & 63);
         const int pb = __builtin_amdgcn_readlane(pw1, rel & 63);
         const int64_t page = rel < 64 ? pa : pb;
         const int64_t off = page * p.cbs + (int64_t)(((16 * sp_of(kt)) % bs) >> 4) * SUBPAGE_BYTES;
-        pf_fetch(rw, kplane + off, vplane + off, lane, hf);
+        pf_fetch(rw.h[0], kplane + off, vplane + off, lane, hf);
+        if constexpr (PF_NSP == 8) pf_fetch(rw.h[1], kplane + off, vplane + off, lane, 1);
+    };
+    auto dequant = [&](const PfRawT &rw, uint8_t *st, auto tail) {
+        constexpr bool T = decltype(tail)::value;
+        pf_dequant<T>(rw.h[0], st, wsp, lane, hf);
+        if constexpr (PF_NSP == 8) pf_dequant<T>(rw.h[1], st, wsp, lane, 1);
     };
 
     float16v_t o[4];
@@ -811,15 +841,23 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
 
     // One pipeline step: loads of tile kt+2 into rf, dequant of tile kt+1
     // from rd, attention over tile kt.
-    auto step = [&](int kt, PfRaw &rf, const PfRaw &rd) {
-        const uint8_t *stage = lds + (kt & 1) * PF_STAGE;
-        fetch(rf, kt + 2);
-        pf_dequant(rd, lds + ((kt + 1) & 1) * PF_STAGE, wsp, lane, hf);
+    // mode: 0 = fetch tile kt+2 and dequantize tile kt+1 (a full tile),
+    //       1 = same, tile kt+1 being the last (tail) tile,
+    //       2 = nothing left to fetch or dequantize
+    auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode) {
+        // odd: kt & 1 (compile time) - read stage kt&1, write stage (kt+1)&1
+        const uint8_t *stage = decltype(odd)::value ? lds1 : lds0;
+        uint8_t *wstage = decltype(odd)::value ? lds0 : lds1;
+        constexpr int MODE = decltype(mode)::value;
+        if constexpr (MODE != 2) {
+            fetch(rf, kt + 2);
+            dequant(rd, wstage, std::integral_constant<bool, MODE == 1>{});
+        }
 
-        // S'^T = K^ . Q^T - m for the two 32-key halves of the tile
-        float16v_t sacc[2];
+        // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile
+        float16v_t sacc[PF_NST];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
+        for (int st = 0; st < PF_NST; ++st) {
             sacc[st] = cneg;
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
@@ -827,10 +865,21 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
+#if GFA_PF_SCHED
+        // interleave the next tile's dequant (VALU + LDS stores) with the QK
+        // MFMAs and their operand reads
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x002, GFA_PF_SCHED, 0);  // VALU
+            if (i % 3 == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+        }
+#endif
         const int kbase_t = PF_TK * kt;
         if (kbase_t + PF_TK - 1 > lim_min) {  // uniform: tile crosses some row's bound
 #pragma unroll
-            for (int st = 0; st < 2; ++st)
+            for (int st = 0; st < PF_NST; ++st)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int key = kbase_t + 32 * st + 8 * (e >> 2) + 4 * hb + (e & 3);
@@ -839,7 +888,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         }
         float mx = sacc[0][0];
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+        for (int st = 0; st < PF_NST; ++st)
 #pragma unroll
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
         {
@@ -858,13 +907,13 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
 #pragma unroll
-            for (int st = 0; st < 2; ++st) sacc[st] -= delta;
+            for (int st = 0; st < PF_NST; ++st) sacc[st] -= delta;
 #pragma unroll
             for (int e = 0; e < 16; ++e) cneg[e] = -m_use;
         }
         const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
+        for (int st = 0; st < PF_NST; ++st) {
 #pragma unroll
             for (int sg = 0; sg < 2; ++sg) {
                 PHalf8 pk;
@@ -886,24 +935,47 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         }
         __syncthreads();
     };
-    PfRaw r0, r1;
+    using Even = std::integral_constant<bool, false>;
+    using Odd = std::integral_constant<bool, true>;
+    using Full = std::integral_constant<int, 0>;
+    using Tail = std::integral_constant<int, 1>;
+    using Last = std::integral_constant<int, 2>;
+    PfRawT r0, r1;
     if (ntk > 0) {
         pw0 = load_pg(0);
         pw1 = ntk > 64 ? load_pg(1) : 0;
         fetch(r0, 0);
-        fetch(r1, 1);
-        pf_dequant(r0, lds, wsp, lane, hf);
+        if (ntk > 1) {
+            fetch(r1, 1);
+            dequant(r0, lds0, std::integral_constant<bool, false>{});
+        } else {
+            dequant(r0, lds0, std::integral_constant<bool, true>{});
+        }
     }
     __syncthreads();
-    for (int kt = 0; kt < ntk; kt += 2) {
-        // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2
-        step(kt, r0, r1);
-        if (kt + 1 < ntk) step(kt + 1, r1, r0);  // uniform
-        if (kt + 2 - cbase >= 64) {             // slide the page windows (uniform)
+    // Main loop: pairs of tiles whose dequantized successors are full tiles.
+    // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2.
+    int kt = 0;
+    for (; kt + 3 < ntk; kt += 2) {
+        step(kt, r0, r1, Even{}, Full{});
+        step(kt + 1, r1, r0, Odd{}, Full{});
+        if (kt + 2 - cbase >= 64) {  // slide the page windows (uniform)
             cbase += 64;
             pw0 = pw1;
             pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
         }
+    }
+    // the last 1-3 tiles (uniform)
+    const int rem = ntk - kt;
+    if (rem == 3) {
+        step(kt, r0, r1, Even{}, Full{});
+        step(kt + 1, r1, r0, Odd{}, Tail{});
+        step(kt + 2, r0, r1, Even{}, Last{});
+    } else if (rem == 2) {
+        step(kt, r0, r1, Even{}, Tail{});
+        step(kt + 1, r1, r0, Odd{}, Last{});
+    } else if (rem == 1) {
+        step(kt, r0, r1, Even{}, Last{});
     }
 
     // normalise and store: register e of d-tile dt is d = 32dt + 8(e/4) + 4hb + e%4
