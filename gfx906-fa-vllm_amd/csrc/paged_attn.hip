@@ -366,10 +366,16 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
 constexpr int DEC_NW = 4;          // waves per decode workgroup
 constexpr int DEC_MIN_UNITS = 16;  // sub-pages per decode workgroup, at least
 
+#ifndef GFA_DEC_DEPTH2
+#define GFA_DEC_DEPTH2 2
+#endif
+#ifndef GFA_DEC_WPE2
+#define GFA_DEC_WPE2 2
+#endif
 template <int NRG>
 struct DecCfg {
-    static constexpr int depth = NRG == 1 ? DEC_DEPTH : 2;
-    static constexpr int wpe = NRG == 1 ? GFA_DEC_WPE : 2;
+    static constexpr int depth = NRG == 1 ? DEC_DEPTH : GFA_DEC_DEPTH2;
+    static constexpr int wpe = NRG == 1 ? GFA_DEC_WPE : GFA_DEC_WPE2;
 };
 
 struct SegInfo {
@@ -552,48 +558,71 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     }
 }
 
-// Merges the partial pieces of split decode segments, from the plan the
-// decode kernel published (U, nwg, per-sequence prefix).  grid (num_seqs, Hkv),
-// block 256: thread -> (row, 4 consecutive d); one-pass online merge, so the
-// loads of all pieces are independent.
+// Merge pass over split segments, from the plan the decode kernel published
+// (U, nwg, per-sequence prefix).  grid (num_seqs, Hkv, 16*NRG rows), block
+// 256: workgroup (s, h, r) merges row r of segment (s, h) when the segment
+// was split.  Thread t owns d-chunk t%32 (4 d) and pieces k = wf + t/32,
+// wf + t/32 + 8, ... (one-pass online merge, independent loads); the 8
+// partial states per d-chunk are then merged through LDS.  Piece k
+// (workgroup k) sits in slot 2k+1 when the segment starts inside k's range
+// (it is k's last piece), else in slot 2k.  (A last-arriver merge inside the
+// decode kernel needs agent-scope release / acquire fences around a
+// per-segment counter; on this part those write back and invalidate the
+// XCD's L2 and made the decode pass 3.5x slower, so the merge stays a
+// second, tiny launch.)
 template <int NRG, int ODT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     constexpr int R = 16 * NRG;
-    const int s = blockIdx.x, h = blockIdx.y;
+    const int s = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
     const SegInfo si = seg_info(p, s);
+    if (si.nsub == 0 || r >= si.nq * p.G) return;
     const int64_t U = p.ws_hdr[0];
     const int nwg = (int)p.ws_hdr[1];
-    const int pre = p.ws_pre[s];
-    if (si.nsub == 0 || U == 0) return;
-    const int64_t S0 = (int64_t)pre * p.Hkv + (int64_t)h * si.nsub;
+    if (U == 0) return;
+    const int64_t S0 = (int64_t)p.ws_pre[s] * p.Hkv + (int64_t)h * si.nsub;
     const int wf = range_of(U, S0, nwg), wl = range_of(U, S0 + si.nsub - 1, nwg);
     if (wf == wl && range_start(U, wf, nwg) <= S0 && range_start(U, wf + 1, nwg) >= S0 + si.nsub)
         return;  // whole segment in one workgroup: already written
-    const int nrows = si.nq * p.G;
-    for (int it = threadIdx.x; it < nrows * 32; it += 256) {
-        const int r = it >> 5, d0 = (it & 31) * 4;
-        float m = -INFINITY, l = 0.f;
-        float4_t o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int k = wf; k <= wl; ++k) {
-            const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
-            const int64_t row = (int64_t)sk * R + r;
-            const float mk = p.ws_ml[2 * row], lk = p.ws_ml[2 * row + 1];
-            const float4_t ok = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
-            const float mn = fmaxf(m, mk);
-            const float ms = mn == -INFINITY ? 0.0f : mn;
-            const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
-            l = l * a + lk * c;
-            o = o * a + ok * c;
-            m = mn;
-        }
-        const int j = r / p.G;
-        const int hq = h * p.G + (r - j * p.G);
-        const int64_t ob = (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
-        const float inv = l > 0.f ? 1.0f / l : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
+    const int t = threadIdx.x, dc = t & 31, sub = t >> 5;
+    const int d0 = 4 * dc;
+    float m = -INFINITY, l = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+    for (int k = wf + sub; k <= wl; k += 8) {
+        const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
+        const int64_t row = (int64_t)sk * R + r;
+        const float mk = p.ws_ml[2 * row], lk = p.ws_ml[2 * row + 1];
+        const float4_t ok = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
+        const float mn = fmaxf(m, mk);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
+        l = l * a + lk * c;
+        o = o * a + ok * c;
+        m = mn;
     }
+    __shared__ float sm[8][32][6];
+    sm[sub][dc][0] = m;
+    sm[sub][dc][1] = l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm[sub][dc][2 + i] = o[i];
+    __syncthreads();
+    if (sub != 0) return;
+#pragma unroll
+    for (int q = 1; q < 8; ++q) {
+        const float mk = sm[q][dc][0], lk = sm[q][dc][1];
+        const float mn = fmaxf(m, mk);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
+        l = l * a + lk * c;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = o[i] * a + sm[q][dc][2 + i] * c;
+        m = mn;
+    }
+    const int j = r / p.G;
+    const int hq = h * p.G + (r - j * p.G);
+    const int64_t ob = (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
+    const float inv = l > 0.f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -1044,10 +1073,10 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     AttnParams p = p0;
     if (pl.dec_nrg == 1) {
         attn_decode_kernel<1, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(p);
+        attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, 16), 256, 0, stream>>>(p);
     } else {
         attn_decode_kernel<2, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(p);
+        attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, 32), 256, 0, stream>>>(p);
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
