@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-prefill]
 
-Headline (``value``): batched decode, BASELINE cfg2 - 32 sequences with
+Headline (``value``): batched decode, cfg2 of the benchmark definition - 32 sequences with
 contexts U[2048, 16384], 48 query / 8 KV heads, head_dim 128, fp16 Q, Q8_0
 K and V, block_size 16, permuted block tables.  One step = quantize-write the
 32 new tokens' K/V into the paged cache + one attention pass over the batch,
@@ -95,7 +95,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the kernel shards by KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(attention shards by KV head with no exchange inside the kernel)", file=sys.stderr)
         return 2
 
     import numpy as np

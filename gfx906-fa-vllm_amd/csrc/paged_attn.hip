@@ -55,7 +55,8 @@ struct AttnParams {
     const void *q;
     int64_t q_ts, q_hs;
     const uint8_t *kc, *vc;
-    int64_t cbs, chs;
+    int64_t cbs, chs;    // K (and Q8 V) plane strides in bytes: page, kv-head
+    int64_t vcbs, vchs;  // V plane strides (equal to cbs, chs for a Q8 V plane)
     const int32_t *bt;
     int64_t bt_stride;
     const int32_t *seq_lens, *qsl, *q_abs;
@@ -698,12 +699,23 @@ struct PfRaw {
     uint32_t ks;
 };
 
+// VF16: V is a planar fp16 sub-page (4096 B; element (t, d) at
+// 2048*(d/64) + 32*(16*(t/4) + d%16) + 8*((d/16)%4) + 2*(t%4)), so the lane's
+// 16 fp16 values (4 d x 4 tokens) are the 32 bytes at 2048*hf + 32*lane:
+// v = the first 16, vs = the second 16.
+template <bool VF16>
 __device__ __forceinline__ void pf_fetch(PfRaw &r, const uint8_t *kb, const uint8_t *vb, int lane, int hf) {
     const int t = lane & 15, g = lane >> 4;
     r.k = *reinterpret_cast<const u32x4 *>(kb + hf * 1024 + (4 * t + g) * 16);
     r.ks = *reinterpret_cast<const uint32_t *>(kb + SCALE_OFF + 8 * t + 4 * hf);
-    r.v = *reinterpret_cast<const u32x4 *>(vb + hf * 1024 + lane * 16);
-    r.vs = *reinterpret_cast<const u32x4 *>(vb + SCALE_OFF + 32 * g + 16 * hf);
+    if constexpr (VF16) {
+        const u32x4 *v = reinterpret_cast<const u32x4 *>(vb + hf * 2048 + lane * 32);
+        r.v = v[0];
+        r.vs = v[1];
+    } else {
+        r.v = *reinterpret_cast<const u32x4 *>(vb + hf * 1024 + lane * 16);
+        r.vs = *reinterpret_cast<const u32x4 *>(vb + SCALE_OFF + 32 * g + 16 * hf);
+    }
 }
 
 __device__ __forceinline__ half8_t scale8(half8_t v, half_t s) {
@@ -723,7 +735,7 @@ __device__ __forceinline__ half2_t finite2(half2_t x) {
 // keys past kv_end): bytes of tokens past the valid range are dequantized as
 // they are - their scores are masked to -inf (P = 0) - and the V scales are
 // made finite so that 0 * V^ stays 0.
-template <bool TAIL>
+template <bool TAIL, bool VF16>
 __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int sp, int lane, int hf) {
     {
         const int t = lane & 15, g = lane >> 4;
@@ -744,6 +756,15 @@ __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int s
         // contraction position 16sp + 8(T&1) + 4(T>>1) (key bits 2 and 3 swapped)
         uint8_t *vcol = stage + PF_KBYTES + (i + 64 * hf) * PF_VPITCH +
                         2 * (16 * sp + 8 * (T & 1) + 4 * (T >> 1));
+        if constexpr (VF16) {  // already fp16: 4 tokens of d = i + 16(4hf + mm) per 8 bytes
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                const uint32_t lo = mm < 2 ? vq[2 * mm] : vsw[2 * mm - 4];
+                const uint32_t hi = mm < 2 ? vq[2 * mm + 1] : vsw[2 * mm - 3];
+                *reinterpret_cast<u32x2 *>(vcol + 16 * mm * PF_VPITCH) = u32x2{lo, hi};
+            }
+            return;
+        }
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) {
             const int b = mm >> 1;  // block 2hf + b: scale dwords 2b (tokens 0,1), 2b+1 (2,3)
@@ -762,7 +783,7 @@ __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int s
     }
 }
 
-template <int QDT, int ODT>
+template <int QDT, int ODT, bool VF16>
 __global__ __launch_bounds__(64 * PF_WAVES)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p) {
     // two LDS stages as distinct objects: the compiler can then prove that
@@ -830,7 +851,8 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
     };
     const uint8_t *kplane = p.kc + (int64_t)h * p.chs;
-    const uint8_t *vplane = p.vc + (int64_t)h * p.chs;
+    const uint8_t *vplane = p.vc + (int64_t)h * p.vchs;
+    constexpr int VSUB = VF16 ? 4096 : SUBPAGE_BYTES;  // V bytes per 16-token sub-page
     int pw0 = 0, pw1 = 0, cbase = 0;
     struct PfRawT {
         PfRaw h[PF_NSP == 8 ? 2 : 1];
@@ -840,14 +862,16 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         const int pa = __builtin_amdgcn_readlane(pw0, rel & 63);
         const int pb = __builtin_amdgcn_readlane(pw1, rel & 63);
         const int64_t page = rel < 64 ? pa : pb;
-        const int64_t off = page * p.cbs + (int64_t)(((16 * sp_of(kt)) % bs) >> 4) * SUBPAGE_BYTES;
-        pf_fetch(rw.h[0], kplane + off, vplane + off, lane, hf);
-        if constexpr (PF_NSP == 8) pf_fetch(rw.h[1], kplane + off, vplane + off, lane, 1);
+        const int64_t spi = ((16 * sp_of(kt)) % bs) >> 4;
+        const uint8_t *kb = kplane + page * p.cbs + spi * SUBPAGE_BYTES;
+        const uint8_t *vb = vplane + page * p.vcbs + spi * VSUB;
+        pf_fetch<VF16>(rw.h[0], kb, vb, lane, hf);
+        if constexpr (PF_NSP == 8) pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
     };
     auto dequant = [&](const PfRawT &rw, uint8_t *st, auto tail) {
         constexpr bool T = decltype(tail)::value;
-        pf_dequant<T>(rw.h[0], st, wsp, lane, hf);
-        if constexpr (PF_NSP == 8) pf_dequant<T>(rw.h[1], st, wsp, lane, 1);
+        pf_dequant<T, VF16>(rw.h[0], st, wsp, lane, hf);
+        if constexpr (PF_NSP == 8) pf_dequant<T, VF16>(rw.h[1], st, wsp, lane, 1);
     };
 
     float16v_t o[4];
@@ -1081,7 +1105,7 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
         const int tiles = (rows + 32 * PF_WAVES - 1) / (32 * PF_WAVES);
-        attn_prefill_kernel<QDT, ODT><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
+        attn_prefill_kernel<QDT, ODT, false><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
     }
     return hipGetLastError();
 }
@@ -1147,6 +1171,8 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     p.vc = v_cache;
     p.cbs = cache_block_stride;
     p.chs = cache_head_stride;
+    p.vcbs = cache_block_stride;
+    p.vchs = cache_head_stride;
     p.bt = block_table;
     p.bt_stride = block_table_stride;
     p.seq_lens = seq_lens;
@@ -1182,3 +1208,69 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     }
 #undef GFA_DISPATCH_O
 }
+
+extern "C" hipError_t gfx906_fa_amd_paged_attention_f16v(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const void *v_cache_f16, int64_t k_block_stride,
+    int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride,
+    const int32_t *block_table, int64_t block_table_stride, const int32_t *seq_lens,
+    const int32_t *query_start_loc, const int32_t *q_abs_offset, int causal, int num_seqs,
+    int num_tokens, int num_heads, int num_kv_heads, int head_size, int block_size,
+    int max_query_len, float scale, void *out, int out_dtype, int64_t out_token_stride,
+    int64_t out_head_stride, hipStream_t stream) {
+    if (num_seqs == 0 || num_tokens == 0) return hipSuccess;
+    if (head_size != 128 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 ||
+        block_size <= 0 || block_size % 16 != 0 || q_dtype < 0 || q_dtype > 2 || out_dtype < 0 ||
+        out_dtype > 2 || max_query_len < 0) {
+        fprintf(stderr, "[gfx906_fa_amd] paged_attention_f16v: unsupported configuration "
+                        "(head_size=%d heads=%d/%d block_size=%d)\n",
+                head_size, num_heads, num_kv_heads, block_size);
+        return hipErrorInvalidValue;
+    }
+    if ((((uintptr_t)k_cache | (uintptr_t)v_cache_f16) | (uint64_t)k_block_stride |
+         (uint64_t)k_head_stride | (uint64_t)v_block_stride | (uint64_t)v_head_stride) & 15u) {
+        fprintf(stderr, "[gfx906_fa_amd] paged_attention_f16v: cache bases and strides must be 16-byte aligned\n");
+        return hipErrorInvalidValue;
+    }
+    AttnParams p = {};
+    p.q = q;
+    p.q_ts = q_token_stride;
+    p.q_hs = q_head_stride;
+    p.kc = k_cache;
+    p.vc = static_cast<const uint8_t *>(v_cache_f16);
+    p.cbs = k_block_stride;
+    p.chs = k_head_stride;
+    p.vcbs = v_block_stride;
+    p.vchs = v_head_stride;
+    p.bt = block_table;
+    p.bt_stride = block_table_stride;
+    p.seq_lens = seq_lens;
+    p.qsl = query_start_loc;
+    p.q_abs = q_abs_offset;
+    p.causal = causal ? 1 : 0;
+    p.Hkv = num_kv_heads;
+    p.G = num_heads / num_kv_heads;
+    p.block_size = block_size;
+    p.scale_log2e = scale * LOG2E;
+    p.out = out;
+    p.o_ts = out_token_stride;
+    p.o_hs = out_head_stride;
+    p.num_seqs = num_seqs;
+    p.dec_rows_max = 0;  // every sequence through the prefill kernel
+    const int rows = max(max_query_len, 1) * p.G;
+    const dim3 grid(((rows + PF_ROWS - 1) / PF_ROWS) * num_kv_heads, num_seqs);
+#define GFA_F16V_O(QDT)                                                                                   \
+    switch (out_dtype) {                                                                                  \
+        case GFA_DTYPE_F32: attn_prefill_kernel<QDT, GFA_DTYPE_F32, true><<<grid, 64 * PF_WAVES, 0, stream>>>(p); break; \
+        case GFA_DTYPE_F16: attn_prefill_kernel<QDT, GFA_DTYPE_F16, true><<<grid, 64 * PF_WAVES, 0, stream>>>(p); break; \
+        default: attn_prefill_kernel<QDT, GFA_DTYPE_BF16, true><<<grid, 64 * PF_WAVES, 0, stream>>>(p); break;        \
+    }
+    switch (q_dtype) {
+        case GFA_DTYPE_F32: GFA_F16V_O(GFA_DTYPE_F32); break;
+        case GFA_DTYPE_F16: GFA_F16V_O(GFA_DTYPE_F16); break;
+        default: GFA_F16V_O(GFA_DTYPE_BF16); break;
+    }
+#undef GFA_F16V_O
+    return hipGetLastError();
+}
+

@@ -14,6 +14,8 @@ quantize_q8_0(k_fp16)                                  extension/gfx906_fa.cpp:2
 reshape_and_cache_q8(key, slot_mapping, k_cache_q8)    extension/gfx906_fa.cpp:322-374
 gather_paged_kv_q8(key_cache_q8, value_cache, block_table, seq_lens, Sk,
                    k_out=None, v_out=None)             extension/gfx906_fa.cpp:393-498
+forward(q, k_q8, v_fp16, scale, kv_max=None, mask=None, q_abs_offset=None)
+                                                       extension/gfx906_fa.cpp:120-265
 forward_paged_direct(q, key_cache_q8, value_cache, block_table, seq_lens,
                      scale, mask=None, q_abs_offset=None)
                                                        extension/gfx906_fa.cpp:516-658
@@ -71,6 +73,9 @@ def _load():
         "gfx906_fa_amd_paged_attention_workspace_size": (SZ, [I, I, I, I, I, I, I]),
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
+        "gfx906_fa_amd_pack_flat_kv": (I, [P, P, P, P, I, I, I, P]),
+        "gfx906_fa_amd_paged_attention_f16v": (I, [P, I, I64, I64, P, P, I64, I64, I64, I64, P, I64, P,
+                                                   P, P, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -367,6 +372,78 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
         _stream(query.device))
     _ok(err, "gfx906_fa_amd_paged_attention")
     return out
+
+
+def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: float,
+            kv_max: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
+            q_abs_offset: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Contiguous attention with the reference signature
+    (``extension/gfx906_fa.cpp:120-265``, bound at 662-666):
+    q fp32 [B, Hq, Sq, D], k_q8 uint8 [B, Hkv, Skv, D/32*34] (AoS Q8_0 rows),
+    v_fp16 fp16 [B, Hkv, Skv, D] -> fp32 [B, Hq, Sq, D].  K is dequantized,
+    V stays fp16, softmax in fp32.  kv_max int32 [B]: every row sees keys
+    < kv_max[b]; q_abs_offset int32 [B]: row j sees keys
+    k <= q_abs_offset[b] + j (inline causal, ``kernel/fattn-q8.cuh:646-653``).
+    A materialised mask is not supported (the reference replaced it with
+    q_abs_offset, ``extension/gfx906_fa_paged.py:400-425``).  D = 128 only,
+    as the reference launcher (``extension/gfx906_fa_launcher.cu:76-79``)."""
+    for t, n in ((q, "q"), (k_q8, "k_q8"), (v_fp16, "v_fp16")):
+        _cuda(t, n)
+        _check(t.is_contiguous(), f"{n} must be contiguous")
+    _check(q.dtype == torch.float32, "q must be fp32")
+    _check(k_q8.dtype == torch.uint8, "k_q8 must be uint8 (block_q8_0 bytes)")
+    _check(v_fp16.dtype == torch.float16, "v_fp16 must be fp16")
+    _check(q.dim() == 4, "q must be 4D [B, Hq, Sq, D]")
+    _check(v_fp16.dim() == 4, "v_fp16 must be 4D [B, Hkv, Skv, D]")
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = v_fp16.shape[1], v_fp16.shape[2]
+    _check(v_fp16.shape[0] == B, "v batch mismatch")
+    _check(v_fp16.shape[3] == D, "v head_dim mismatch")
+    _check(D % QK8_0 == 0, "head_dim must be multiple of 32")
+    _check(k_q8.dim() == 4 and tuple(k_q8.shape[:3]) == (B, Hkv, Skv),
+           "k_q8 first 3 dims must match [B, Hkv, Skv]")
+    _check(k_q8.shape[3] == D // QK8_0 * Q8_0_BYTES, "k_q8 last dim = (D/32)*34 bytes")
+    _check(D == 128, f"head_dim={D} unsupported (only 128)")
+    _check(Hq % Hkv == 0, f"heads_q={Hq} must be divisible by heads_kv={Hkv}")
+    _check(mask is None, "mask is not supported: use q_abs_offset (inline causal)")
+    dev = q.device
+    out = torch.empty((B * Sq, Hq, D), dtype=torch.float32, device=dev)
+    if B == 0 or Sq == 0 or Hq == 0:
+        return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
+    if kv_max is not None:
+        _cuda(kv_max, "kv_max")
+        _check(kv_max.dtype == torch.int32, "kv_max must be int32")
+        _check(kv_max.dim() == 1 and kv_max.shape[0] == B, "kv_max must be 1D [B]")
+        sl = kv_max.clamp(0, Skv).to(torch.int32).contiguous()
+    else:
+        sl = torch.full((B,), Skv, dtype=torch.int32, device=dev)
+    if q_abs_offset is not None:
+        _cuda(q_abs_offset, "q_abs_offset")
+        _check(q_abs_offset.dtype == torch.int32 and q_abs_offset.dim() == 1 and q_abs_offset.shape[0] == B,
+               "q_abs_offset must be 1D [B]")
+        q_abs_offset = q_abs_offset.contiguous()
+    skp = (max(Skv, 1) + SUBPAGE_TOKENS - 1) // SUBPAGE_TOKENS
+    kp = torch.empty((B, Hkv, skp * SUBPAGE_BYTES), dtype=torch.uint8, device=dev)
+    vp = torch.empty((B, Hkv, skp * 4096), dtype=torch.uint8, device=dev)
+    L = _load()
+    st = _stream(dev)
+    if Skv > 0:
+        _ok(L.gfx906_fa_amd_pack_flat_kv(_ptr(k_q8), _ptr(v_fp16), _ptr(kp), _ptr(vp), B * Hkv, Skv, D, st),
+            "gfx906_fa_amd_pack_flat_kv")
+    else:
+        kp.zero_()
+        vp.zero_()
+    bt = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
+    qsl = torch.arange(0, (B + 1) * Sq, Sq, dtype=torch.int32, device=dev)
+    q_bshd = q.transpose(1, 2).contiguous().view(B * Sq, Hq, D)
+    err = L.gfx906_fa_amd_paged_attention_f16v(
+        _ptr(q_bshd), _DT[torch.float32], q_bshd.stride(0), q_bshd.stride(1), _ptr(kp), _ptr(vp),
+        kp.stride(0), kp.stride(1), vp.stride(0), vp.stride(1), _ptr(bt), 1, _ptr(sl), _ptr(qsl),
+        _ptr(q_abs_offset), 1 if q_abs_offset is not None else 0, B, B * Sq, Hq, Hkv, D,
+        skp * SUBPAGE_TOKENS, Sq, float(scale), _ptr(out), _DT[torch.float32], out.stride(0),
+        out.stride(1), st)
+    _ok(err, "gfx906_fa_amd_paged_attention_f16v")
+    return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
 
 
 def forward_paged_direct(q: torch.Tensor, key_cache_q8: torch.Tensor, value_cache: torch.Tensor,

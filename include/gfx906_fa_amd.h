@@ -189,6 +189,40 @@ hipError_t gfx906_fa_amd_paged_attention(
     void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
     void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * (6) Repack the reference's contiguous attention inputs for (7):
+ *       k_aos [rows, Skv, 136] AoS Q8_0 K rows -> k_planar [rows, Skv_pad/16, 2176]
+ *       v_f16 [rows, Skv, 128] fp16 V rows     -> v_planar [rows, Skv_pad/16, 4096]
+ *     rows = B * Hkv (sequence-major), Skv_pad = Skv rounded up to 16; the
+ *     padding tokens are written as zeros.  K bytes are permuted, never
+ *     changed.  fp16 V sub-page layout: element (t, d) at byte
+ *       2048*(d/64) + 32*(16*(t/4) + d%16) + 8*((d/16)%4) + 2*(t%4).
+ *     Serves the contiguous entry gfx906_fa_forward
+ *     (extension/gfx906_fa.cpp:120-265, launcher extension/gfx906_fa_launcher.cu:53-209),
+ *     whose V stays fp16.
+ */
+hipError_t gfx906_fa_amd_pack_flat_kv(const uint8_t *k_aos, const void *v_f16,
+                                      uint8_t *k_planar, void *v_planar, int rows, int Skv,
+                                      int head_size, hipStream_t stream);
+
+/* (7) Paged attention with a planar Q8 K plane and a planar fp16 V plane
+ *     (layout of (6)), separate K / V page and kv-head strides (bytes).
+ *     Semantics as (5): dequantized K, exact fp16 V, fp32 softmax; every
+ *     sequence runs through the tiled (prefill) kernel, no workspace.  With
+ *     (6) and block_size = Skv_pad this is the contiguous attention of
+ *     gfx906_fa_launch (extension/gfx906_fa_launcher.cu:53-209): kv_max maps
+ *     to seq_lens, q_abs_offset to the inline causal bound.
+ */
+hipError_t gfx906_fa_amd_paged_attention_f16v(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const void *v_cache_f16, int64_t k_block_stride,
+    int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride,
+    const int32_t *block_table, int64_t block_table_stride, const int32_t *seq_lens,
+    const int32_t *query_start_loc, const int32_t *q_abs_offset, int causal, int num_seqs,
+    int num_tokens, int num_heads, int num_kv_heads, int head_size, int block_size,
+    int max_query_len, float scale, void *out, int out_dtype, int64_t out_token_stride,
+    int64_t out_head_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,8 +33,15 @@ Pinning (what checks each function beyond restating it):
   Pinned by: torch SDPA (math backend, float64) on the same dequantized
   inputs, a single visible key giving the V row, uniform scores giving the
   mean of V, invariance to block_table permutation.
-* ``planar_*`` - the MI355X page layout of this build (not a reference
-  format); pinned by round trips against the AoS rows.
+* ``flat_attention_ref`` - the contiguous path of the op module's
+  ``forward`` (``extension/gfx906_fa.cpp:120-265``): dequantized K, exact
+  fp16 V, kv_max cutoff and inline causal bound.  Pinned by: torch SDPA
+  (math backend, float64) with the equivalent boolean mask, a single visible
+  key giving the V row, and agreement with ``paged_attention_ref`` on the
+  same dequantized values laid out as pages.
+* ``planar_*`` - the MI355X page layouts of this build (not reference
+  formats); pinned by round trips against the AoS / fp16 rows (each
+  position map a bijection onto its sub-page).
 """
 from __future__ import annotations
 
@@ -355,7 +362,7 @@ def paged_attention_ref(query: np.ndarray, k_hat: np.ndarray, v_hat: np.ndarray,
     (``extension/gfx906_fa_paged.py:288-295``, ``kernel/fattn-q8.cuh:646-653``);
     q-head h reads kv-head h // (Hq/Hkv) (``kernel/fattn-q8.cuh:898-901``).
     A row with no visible key outputs 0 (``seq_len = 0``; the reference
-    divides by zero there, SURVEY D9)."""
+    divides by zero there)."""
     T, Hq, D = query.shape
     NB, bs, Hkv, _ = k_hat.shape
     G = Hq // Hkv
@@ -387,6 +394,51 @@ def paged_attention_ref(query: np.ndarray, k_hat: np.ndarray, v_hat: np.ndarray,
             o = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
             out[q0:q1, h * G:(h + 1) * G, :] = o
     return out
+
+
+def flat_attention_ref(q: np.ndarray, k_aos: np.ndarray, v: np.ndarray, scale: float,
+                       kv_max=None, q_abs_offset=None) -> np.ndarray:
+    """Contiguous attention of the op module's ``forward``
+    (``extension/gfx906_fa.cpp:120-265``; kernel ``kernel/fattn-q8.cuh:835-1087``)
+    over dequantized K and exact fp16 V, float64 softmax.
+
+    q [B, Hq, Sq, D]; k_aos uint8 [B, Hkv, Skv, D/32*34]; v [B, Hkv, Skv, D]
+    -> [B, Hq, Sq, D].  Row j of batch b sees key k when k < kv_max[b] (all
+    Skv keys without kv_max; ``extension/gfx906_fa.cpp:189-212``) and, with
+    q_abs_offset, k <= q_abs_offset[b] + j (``kernel/fattn-q8.cuh:646-653``).
+    q-head h reads kv-head h // (Hq/Hkv) (``kernel/fattn-q8.cuh:898-901``).
+    A row with no visible key outputs 0."""
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = v.shape[1], v.shape[2]
+    G = Hq // Hkv
+    K = dequantize_q8_0_rows(k_aos, D).astype(np.float64)   # [B, Hkv, Skv, D]
+    V = np.asarray(v, dtype=np.float64)
+    out = np.zeros((B, Hq, Sq, D), dtype=np.float64)
+    pos = np.arange(Skv)
+    for b in range(B):
+        cut = Skv if kv_max is None else min(max(int(kv_max[b]), 0), Skv)
+        vis = np.broadcast_to(pos[None, :] < cut, (Sq, Skv))
+        if q_abs_offset is not None:
+            vis = vis & (pos[None, :] <= int(q_abs_offset[b]) + np.arange(Sq)[:, None])
+        for h in range(Hkv):
+            qh = q[b, h * G:(h + 1) * G].astype(np.float64)           # [G, Sq, D]
+            sc = np.einsum("gjd,kd->gjk", qh, K[b, h]) * scale
+            sc = np.where(vis[None], sc, -np.inf)
+            m = np.max(sc, axis=-1, keepdims=True)
+            m = np.where(np.isfinite(m), m, 0.0)
+            p = np.where(vis[None], np.exp(sc - m), 0.0)
+            l = p.sum(-1, keepdims=True)
+            o = np.einsum("gjk,kd->gjd", p, V[b, h])
+            out[b, h * G:(h + 1) * G] = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
+    return out
+
+
+def planar_v16_pos(t, d) -> np.ndarray:
+    """Byte offset of fp16 V element (t, d) inside a 4096-byte planar fp16
+    sub-page (the layout of the flat entry's repacked V)."""
+    t = np.asarray(t)
+    d = np.asarray(d)
+    return 2048 * (d // 64) + 32 * (16 * (t // 4) + d % 16) + 8 * ((d // 16) % 4) + 2 * (t % 4)
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,98 @@
+"""GPU: the contiguous entry ``gfx906_fa.forward`` (the reference's
+``extension/gfx906_fa.cpp:120-265``: AoS Q8_0 K, fp16 V) against
+``oracle.flat_attention_ref``, and the repack kernels it uses, bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import gfx906_fa
+from gpu_common import announce, assert_close, need_gpu
+from oracle import q8_oracle as O
+
+DEV = "cuda"
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(seed, B, Hq, Hkv, Sq, Skv):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
+    return q, O.quantize_q8_0_rows(k), v
+
+
+def test_pack_flat_kv_bitexact():
+    need_gpu()
+    announce("pack_flat_kv B=2 Hkv=3 Skv=37")
+    B, Hkv, Skv = 2, 3, 37
+    _, kq, v = _inputs(1, B, 3, Hkv, 1, Skv)
+    skp = (Skv + 15) // 16
+    kp = torch.full((B, Hkv, skp * 2176), 0xAB, dtype=torch.uint8, device=DEV)
+    vp = torch.full((B, Hkv, skp * 4096), 0xAB, dtype=torch.uint8, device=DEV)
+    L = gfx906_fa.lib()
+    kd, vd = torch.from_numpy(kq).to(DEV), torch.from_numpy(v).to(DEV)  # alive across the launch
+    err = L.gfx906_fa_amd_pack_flat_kv(gfx906_fa._ptr(kd), gfx906_fa._ptr(vd), gfx906_fa._ptr(kp),
+                                      gfx906_fa._ptr(vp), B * Hkv, Skv, 128,
+                                      gfx906_fa._stream(torch.device(DEV)))
+    assert err == 0
+    torch.cuda.synchronize()
+    kp, vp = kp.cpu().numpy(), vp.cpu().numpy()
+    qk, dk = O.unpack_q8_0_rows(kq, 128)
+    dd = np.arange(128)
+    vbits = v.view(np.uint16)
+    for b in range(B):
+        for h in range(Hkv):
+            for t in range(skp * 16):
+                sp, tt = divmod(t, 16)
+                base = sp * 2176
+                ints = kp[b, h, base + O.planar_kpos(tt, dd)].view(np.int8)
+                sc = np.array([kp[b, h, base + O.planar_spos(0, tt, bb) + np.arange(2)] for bb in range(4)])
+                vv = vp[b, h, sp * 4096 + O.planar_v16_pos(tt, dd)[:, None] + np.arange(2)].copy().view(np.uint16)[:, 0]
+                if t < Skv:
+                    assert np.array_equal(ints, qk[b, h, t])
+                    assert np.array_equal(sc.copy().view("<f2").ravel(), dk[b, h, t])
+                    assert np.array_equal(vv, vbits[b, h, t])
+                else:  # padding tokens are zeros
+                    assert not ints.any() and not sc.any() and not vv.any()
+
+
+CASES = [
+    # name, B, Hq, Hkv, Sq, Skv, kv_max, causal
+    ("decode", 3, 8, 2, 1, 300, None, False),
+    ("decode_kvmax", 3, 8, 2, 1, 300, [300, 17, 1], False),
+    ("prefill_sq64_causal", 1, 8, 4, 64, 64, None, True),
+    ("sweep_sq512", 1, 8, 4, 512, 1024, None, False),
+    ("gqa_48_8_causal_ragged", 2, 48, 8, 100, 777, [777, 500], True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_forward_flat(case):
+    need_gpu()
+    name, B, Hq, Hkv, Sq, Skv, kv_max, causal = case
+    announce(f"forward {name}")
+    q, kq, v = _inputs(sum(map(ord, name)), B, Hq, Hkv, Sq, Skv)
+    scale = 1.0 / np.sqrt(128)
+    kvm = None if kv_max is None else np.asarray(kv_max, np.int32)
+    qa = None
+    if causal:  # the last Sq positions of each (possibly cut) sequence
+        lens = np.full(B, Skv, np.int32) if kvm is None else kvm
+        qa = (lens - Sq).astype(np.int32)
+    out = gfx906_fa.forward(torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV),
+                            torch.from_numpy(v).to(DEV), scale,
+                            kv_max=None if kvm is None else torch.from_numpy(kvm).to(DEV),
+                            q_abs_offset=None if qa is None else torch.from_numpy(qa).to(DEV))
+    torch.cuda.synchronize()
+    assert out.shape == (B, Hq, Sq, 128) and out.dtype == torch.float32
+    ref = O.flat_attention_ref(q, kq, v, scale, kv_max=kvm, q_abs_offset=qa)
+    assert_close(out.cpu().numpy(), ref)
+
+
+def test_forward_flat_rejects_mask_and_bad_dims():
+    need_gpu()
+    q, kq, v = _inputs(3, 1, 2, 1, 4, 32)
+    args = (torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV), torch.from_numpy(v).to(DEV), 0.1)
+    with pytest.raises(RuntimeError, match="mask"):
+        gfx906_fa.forward(*args, mask=torch.zeros((1, 4, 32), dtype=torch.float16, device=DEV))
+    with pytest.raises(RuntimeError, match="fp32"):
+        gfx906_fa.forward(args[0].half(), *args[1:])

@@ -218,3 +218,60 @@ def test_cpu_baseline_matches_oracle():
     secs, tokens, nseq, passes, thr = CB.time_cpu_decode(torch.from_numpy(q), ka, va, bt, np.asarray(seq_lens),
                                                          np.asarray(q_lens), 0.09, budget_s=0.05)
     assert nseq >= 1 and tokens >= 40 and secs > 0
+
+
+def _flat_case(rng, B, Hq, Hkv, Sq, Skv):
+    q = rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
+    return q, O.quantize_q8_0_rows(k), v
+
+
+def test_flat_attention_oracle_matches_sdpa():
+    rng = np.random.default_rng(9)
+    q, kq, v = _flat_case(rng, 2, 6, 2, 5, 40)
+    kv_max = np.array([40, 23], np.int32)
+    qa = np.array([30, 3], np.int32)
+    got = O.flat_attention_ref(q, kq, v, 0.1, kv_max=kv_max, q_abs_offset=qa)
+    K = torch.from_numpy(O.dequantize_q8_0_rows(kq, 128)).double().repeat_interleave(3, dim=1)
+    V = torch.from_numpy(v.astype(np.float64)).repeat_interleave(3, dim=1)
+    pos = torch.arange(40)
+    for b in range(2):
+        mask = (pos[None, :] < int(kv_max[b])) & (pos[None, :] <= int(qa[b]) + torch.arange(5)[:, None])
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(q[b:b + 1]).double(), K[b:b + 1], V[b:b + 1], attn_mask=mask[None, None], scale=0.1)
+        assert np.max(np.abs(got[b] - ref[0].numpy())) < 1e-10
+    # single visible key -> that key's V row (batch 1, row 0 sees keys <= 3 ... cut by q_abs 3)
+    one = O.flat_attention_ref(q, kq, v, 0.1, kv_max=np.array([1, 1], np.int32))
+    assert np.allclose(one[0, 0, 0], v[0, 0, 0].astype(np.float64))
+    assert np.allclose(one[1, 5, 4], v[1, 1, 0].astype(np.float64))
+
+
+def test_flat_attention_oracle_matches_paged_oracle():
+    """Same values as pages: flat (exact V = dequantized Q8 V) == paged oracle."""
+    rng = np.random.default_rng(10)
+    B, Hq, Hkv, Sq, Skv = 2, 4, 2, 3, 48
+    q = rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32)
+    kq = O.quantize_q8_0_rows(rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16))
+    vq = O.quantize_q8_0_rows(rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16))
+    vh = O.dequantize_q8_0_rows(vq, 128)
+    flat = O.flat_attention_ref(q, kq, vh, 0.08, q_abs_offset=np.full(B, Skv - Sq, np.int32))
+    # pages of 16 tokens, sequence b owns pages b*3 .. b*3+2
+    kh = O.dequantize_q8_0_rows(kq, 128)
+    kpg = kh.transpose(0, 2, 1, 3).reshape(B * 3, 16, Hkv, 128)
+    vpg = vh.transpose(0, 2, 1, 3).reshape(B * 3, 16, Hkv, 128)
+    bt = np.arange(B * 3, dtype=np.int32).reshape(B, 3)
+    paged = O.paged_attention_ref(q.transpose(0, 2, 1, 3).reshape(B * Sq, Hq, 128), kpg, vpg, bt,
+                                  np.full(B, Skv, np.int32), np.arange(0, (B + 1) * Sq, Sq, dtype=np.int32), 0.08)
+    assert np.max(np.abs(flat.transpose(0, 2, 1, 3).reshape(B * Sq, Hq, 128) - paged)) < 1e-12
+
+
+def test_planar_v16_layout_bijection():
+    tt, dd = np.meshgrid(np.arange(16), np.arange(128), indexing="ij")
+    pos = O.planar_v16_pos(tt, dd).ravel()
+    assert sorted(pos.tolist()) == list(range(0, 4096, 2))
+    # a lane's 32 bytes: tokens 4T..4T+3 x d = i + 16(4hf + mm), mm = 0..3
+    lane, hf = 21, 1
+    T, i = lane // 16, lane % 16
+    got = sorted(int(O.planar_v16_pos(4 * T + s, i + 16 * (4 * hf + mm))) for s in range(4) for mm in range(4))
+    assert got == list(range(2048 * hf + 32 * lane, 2048 * hf + 32 * lane + 32, 2))
