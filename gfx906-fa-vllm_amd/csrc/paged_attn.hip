@@ -57,6 +57,9 @@ struct AttnParams {
     const uint8_t *kc, *vc;
     int64_t cbs, chs;    // K (and Q8 V) plane strides in bytes: page, kv-head
     int64_t vcbs, vchs;  // V plane strides (equal to cbs, chs for a Q8 V plane)
+    const uint16_t *mask;             // optional additive fp16 mask [B][n_q][mask_cols]
+    int64_t mask_bs, mask_rs;         // its batch and row strides (elements)
+    int mask_cols;                    // keys it covers
     const int32_t *bt;
     int64_t bt_stride;
     const int32_t *seq_lens, *qsl, *q_abs;
@@ -783,7 +786,7 @@ __device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int s
     }
 }
 
-template <int QDT, int ODT, bool VF16>
+template <int QDT, int ODT, bool VF16, bool MASK>
 __global__ __launch_bounds__(64 * PF_WAVES)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p) {
     // two LDS stages as distinct objects: the compiler can then prove that
@@ -930,6 +933,17 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         }
 #endif
         const int kbase_t = PF_TK * kt;
+        if constexpr (MASK) {  // S' += mask[s][j][key] (natural log units -> log2)
+            const uint16_t *mrow = p.mask + (int64_t)s * p.mask_bs + (int64_t)j * p.mask_rs;
+#pragma unroll
+            for (int st = 0; st < PF_NST; ++st)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = kbase_t + 32 * st + 8 * (e >> 2) + 4 * hb + (e & 3);
+                    const float mv = key < p.mask_cols ? half_bits_to_f32(mrow[key]) : 0.0f;
+                    sacc[st][e] = fmaf(mv, LOG2E, sacc[st][e]);
+                }
+        }
         if (kbase_t + PF_TK - 1 > lim_min) {  // uniform: tile crosses some row's bound
 #pragma unroll
             for (int st = 0; st < PF_NST; ++st)
@@ -1105,7 +1119,7 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
         const int tiles = (rows + 32 * PF_WAVES - 1) / (32 * PF_WAVES);
-        attn_prefill_kernel<QDT, ODT, false><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
+        attn_prefill_kernel<QDT, ODT, false, false><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
     }
     return hipGetLastError();
 }
@@ -1209,27 +1223,28 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
 #undef GFA_DISPATCH_O
 }
 
-extern "C" hipError_t gfx906_fa_amd_paged_attention_f16v(
+extern "C" hipError_t gfx906_fa_amd_paged_attention_tiled(
     const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
-    const uint8_t *k_cache, const void *v_cache_f16, int64_t k_block_stride,
+    const uint8_t *k_cache, const void *v_cache, int v_format, int64_t k_block_stride,
     int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride,
     const int32_t *block_table, int64_t block_table_stride, const int32_t *seq_lens,
-    const int32_t *query_start_loc, const int32_t *q_abs_offset, int causal, int num_seqs,
-    int num_tokens, int num_heads, int num_kv_heads, int head_size, int block_size,
-    int max_query_len, float scale, void *out, int out_dtype, int64_t out_token_stride,
+    const int32_t *query_start_loc, const int32_t *q_abs_offset, int causal,
+    const void *mask, int64_t mask_batch_stride, int64_t mask_row_stride, int mask_cols,
+    int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
+    int block_size, int max_query_len, float scale, float *out, int64_t out_token_stride,
     int64_t out_head_stride, hipStream_t stream) {
     if (num_seqs == 0 || num_tokens == 0) return hipSuccess;
     if (head_size != 128 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 ||
-        block_size <= 0 || block_size % 16 != 0 || q_dtype < 0 || q_dtype > 2 || out_dtype < 0 ||
-        out_dtype > 2 || max_query_len < 0) {
-        fprintf(stderr, "[gfx906_fa_amd] paged_attention_f16v: unsupported configuration "
-                        "(head_size=%d heads=%d/%d block_size=%d)\n",
-                head_size, num_heads, num_kv_heads, block_size);
+        block_size <= 0 || block_size % 16 != 0 || q_dtype < 0 || q_dtype > 2 ||
+        (v_format != 0 && v_format != 1) || max_query_len < 0 || (mask && mask_cols < 0)) {
+        fprintf(stderr, "[gfx906_fa_amd] paged_attention_tiled: unsupported configuration "
+                        "(head_size=%d heads=%d/%d block_size=%d v_format=%d)\n",
+                head_size, num_heads, num_kv_heads, block_size, v_format);
         return hipErrorInvalidValue;
     }
-    if ((((uintptr_t)k_cache | (uintptr_t)v_cache_f16) | (uint64_t)k_block_stride |
+    if ((((uintptr_t)k_cache | (uintptr_t)v_cache) | (uint64_t)k_block_stride |
          (uint64_t)k_head_stride | (uint64_t)v_block_stride | (uint64_t)v_head_stride) & 15u) {
-        fprintf(stderr, "[gfx906_fa_amd] paged_attention_f16v: cache bases and strides must be 16-byte aligned\n");
+        fprintf(stderr, "[gfx906_fa_amd] paged_attention_tiled: cache bases and strides must be 16-byte aligned\n");
         return hipErrorInvalidValue;
     }
     AttnParams p = {};
@@ -1237,7 +1252,7 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_f16v(
     p.q_ts = q_token_stride;
     p.q_hs = q_head_stride;
     p.kc = k_cache;
-    p.vc = static_cast<const uint8_t *>(v_cache_f16);
+    p.vc = static_cast<const uint8_t *>(v_cache);
     p.cbs = k_block_stride;
     p.chs = k_head_stride;
     p.vcbs = v_block_stride;
@@ -1248,6 +1263,10 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_f16v(
     p.qsl = query_start_loc;
     p.q_abs = q_abs_offset;
     p.causal = causal ? 1 : 0;
+    p.mask = static_cast<const uint16_t *>(mask);
+    p.mask_bs = mask_batch_stride;
+    p.mask_rs = mask_row_stride;
+    p.mask_cols = mask_cols;
     p.Hkv = num_kv_heads;
     p.G = num_heads / num_kv_heads;
     p.block_size = block_size;
@@ -1256,21 +1275,23 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_f16v(
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
     p.num_seqs = num_seqs;
-    p.dec_rows_max = 0;  // every sequence through the prefill kernel
+    p.dec_rows_max = 0;  // every sequence through the tiled kernel
     const int rows = max(max_query_len, 1) * p.G;
     const dim3 grid(((rows + PF_ROWS - 1) / PF_ROWS) * num_kv_heads, num_seqs);
-#define GFA_F16V_O(QDT)                                                                                   \
-    switch (out_dtype) {                                                                                  \
-        case GFA_DTYPE_F32: attn_prefill_kernel<QDT, GFA_DTYPE_F32, true><<<grid, 64 * PF_WAVES, 0, stream>>>(p); break; \
-        case GFA_DTYPE_F16: attn_prefill_kernel<QDT, GFA_DTYPE_F16, true><<<grid, 64 * PF_WAVES, 0, stream>>>(p); break; \
-        default: attn_prefill_kernel<QDT, GFA_DTYPE_BF16, true><<<grid, 64 * PF_WAVES, 0, stream>>>(p); break;        \
+    const dim3 block(64 * PF_WAVES);
+#define GFA_TILED(QDT)                                                                                      \
+    if (v_format == 1) {                                                                                    \
+        if (mask) attn_prefill_kernel<QDT, GFA_DTYPE_F32, true, true><<<grid, block, 0, stream>>>(p);       \
+        else attn_prefill_kernel<QDT, GFA_DTYPE_F32, true, false><<<grid, block, 0, stream>>>(p);           \
+    } else {                                                                                                \
+        if (mask) attn_prefill_kernel<QDT, GFA_DTYPE_F32, false, true><<<grid, block, 0, stream>>>(p);      \
+        else attn_prefill_kernel<QDT, GFA_DTYPE_F32, false, false><<<grid, block, 0, stream>>>(p);          \
     }
     switch (q_dtype) {
-        case GFA_DTYPE_F32: GFA_F16V_O(GFA_DTYPE_F32); break;
-        case GFA_DTYPE_F16: GFA_F16V_O(GFA_DTYPE_F16); break;
-        default: GFA_F16V_O(GFA_DTYPE_BF16); break;
+        case GFA_DTYPE_F32: GFA_TILED(GFA_DTYPE_F32); break;
+        case GFA_DTYPE_F16: GFA_TILED(GFA_DTYPE_F16); break;
+        default: GFA_TILED(GFA_DTYPE_BF16); break;
     }
-#undef GFA_F16V_O
+#undef GFA_TILED
     return hipGetLastError();
 }
-

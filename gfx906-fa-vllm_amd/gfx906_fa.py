@@ -74,8 +74,9 @@ def _load():
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
         "gfx906_fa_amd_pack_flat_kv": (I, [P, P, P, P, I, I, I, P]),
-        "gfx906_fa_amd_paged_attention_f16v": (I, [P, I, I64, I64, P, P, I64, I64, I64, I64, P, I64, P,
-                                                   P, P, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P]),
+        "gfx906_fa_amd_paged_attention_tiled": (I, [P, I, I64, I64, P, P, I, I64, I64, I64, I64, P, I64,
+                                                    P, P, P, I, P, I64, I64, I, I, I, I, I, I, I, I,
+                                                    F, P, I64, I64, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -374,6 +375,22 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     return out
 
 
+def _mask_args(mask: Optional[torch.Tensor], B: int, Sq: int, q_abs_offset):
+    """fp16 additive mask [B, Sq, Skv_pad] (``extension/gfx906_fa.cpp:214-227``)
+    -> (tensor, batch stride, row stride, columns) for the tiled entry."""
+    if mask is None:
+        return None, 0, 0, 0
+    _check(q_abs_offset is None,
+           "q_abs_offset and mask are mutually exclusive (inline causal replaces mask)")
+    _cuda(mask, "mask")
+    _check(mask.dtype == torch.float16, "mask must be fp16")
+    _check(mask.dim() == 3, "mask must be 3D [B, Sq, Skv_pad]")
+    _check(mask.shape[0] == B, "mask.size(0) must equal batch")
+    _check(mask.shape[1] == Sq, "mask.size(1) must equal seq_q")
+    m = mask.contiguous()
+    return m, m.stride(0), m.stride(1), m.shape[2]
+
+
 def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: float,
             kv_max: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
             q_abs_offset: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -383,10 +400,10 @@ def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: fl
     v_fp16 fp16 [B, Hkv, Skv, D] -> fp32 [B, Hq, Sq, D].  K is dequantized,
     V stays fp16, softmax in fp32.  kv_max int32 [B]: every row sees keys
     < kv_max[b]; q_abs_offset int32 [B]: row j sees keys
-    k <= q_abs_offset[b] + j (inline causal, ``kernel/fattn-q8.cuh:646-653``).
-    A materialised mask is not supported (the reference replaced it with
-    q_abs_offset, ``extension/gfx906_fa_paged.py:400-425``).  D = 128 only,
-    as the reference launcher (``extension/gfx906_fa_launcher.cu:76-79``)."""
+    k <= q_abs_offset[b] + j (inline causal, ``kernel/fattn-q8.cuh:646-653``);
+    mask fp16 [B, Sq, Skv_pad]: added to the scaled scores
+    (``kernel/fattn-q8.cuh:643-644``), exclusive with q_abs_offset.  D = 128
+    only, as the reference launcher (``extension/gfx906_fa_launcher.cu:76-79``)."""
     for t, n in ((q, "q"), (k_q8, "k_q8"), (v_fp16, "v_fp16")):
         _cuda(t, n)
         _check(t.is_contiguous(), f"{n} must be contiguous")
@@ -405,7 +422,8 @@ def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: fl
     _check(k_q8.shape[3] == D // QK8_0 * Q8_0_BYTES, "k_q8 last dim = (D/32)*34 bytes")
     _check(D == 128, f"head_dim={D} unsupported (only 128)")
     _check(Hq % Hkv == 0, f"heads_q={Hq} must be divisible by heads_kv={Hkv}")
-    _check(mask is None, "mask is not supported: use q_abs_offset (inline causal)")
+    _check(mask is None or mask.dim() != 3 or mask.shape[2] >= Skv, "mask.size(2) must be >= seq_kv")
+    mk, mbs, mrs, mcols = _mask_args(mask, B, Sq, q_abs_offset)
     dev = q.device
     out = torch.empty((B * Sq, Hq, D), dtype=torch.float32, device=dev)
     if B == 0 or Sq == 0 or Hq == 0:
@@ -436,13 +454,13 @@ def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: fl
     bt = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
     qsl = torch.arange(0, (B + 1) * Sq, Sq, dtype=torch.int32, device=dev)
     q_bshd = q.transpose(1, 2).contiguous().view(B * Sq, Hq, D)
-    err = L.gfx906_fa_amd_paged_attention_f16v(
-        _ptr(q_bshd), _DT[torch.float32], q_bshd.stride(0), q_bshd.stride(1), _ptr(kp), _ptr(vp),
+    err = L.gfx906_fa_amd_paged_attention_tiled(
+        _ptr(q_bshd), _DT[torch.float32], q_bshd.stride(0), q_bshd.stride(1), _ptr(kp), _ptr(vp), 1,
         kp.stride(0), kp.stride(1), vp.stride(0), vp.stride(1), _ptr(bt), 1, _ptr(sl), _ptr(qsl),
-        _ptr(q_abs_offset), 1 if q_abs_offset is not None else 0, B, B * Sq, Hq, Hkv, D,
-        skp * SUBPAGE_TOKENS, Sq, float(scale), _ptr(out), _DT[torch.float32], out.stride(0),
+        _ptr(q_abs_offset), 1 if q_abs_offset is not None else 0, _ptr(mk), mbs, mrs, mcols,
+        B, B * Sq, Hq, Hkv, D, skp * SUBPAGE_TOKENS, Sq, float(scale), _ptr(out), out.stride(0),
         out.stride(1), st)
-    _ok(err, "gfx906_fa_amd_paged_attention_f16v")
+    _ok(err, "gfx906_fa_amd_paged_attention_tiled")
     return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
 
 
@@ -456,9 +474,8 @@ def forward_paged_direct(q: torch.Tensor, key_cache_q8: torch.Tensor, value_cach
     of this backend (V is Q8_0 too).  Without q_abs_offset every row sees all
     seq_lens[b] keys (``kv_max`` cutoff); with it, row j sees keys
     k <= q_abs_offset[b] + j (inline causal, ``kernel/fattn-q8.cuh:646-653``).
-    A materialised mask is not supported (the reference replaced it with
-    q_abs_offset, ``extension/gfx906_fa_paged.py:400-425``)."""
-    _check(mask is None, "mask is not supported: use q_abs_offset (inline causal)")
+    mask fp16 [B, Sq, Skv_pad] is added to the scaled scores
+    (``kernel/fattn-q8.cuh:643-644``); exclusive with q_abs_offset."""
     _cuda(q, "q")
     _check(q.dim() == 4, "q must be 4D [B, Hq, Sq, D]")
     B, Hq, Sq, D = q.shape
@@ -469,9 +486,26 @@ def forward_paged_direct(q: torch.Tensor, key_cache_q8: torch.Tensor, value_cach
     bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
     max_kv = bt.shape[1] * (key_cache_q8.shape[2] // SUBPAGE_BYTES * SUBPAGE_TOKENS)
-    out = paged_attention(q_bshd, key_cache_q8, value_cache, bt.contiguous(), sl.contiguous(), qsl,
-                          Sq, max_kv, scale, q_abs_offset=q_abs_offset,
-                          causal=q_abs_offset is not None, out_dtype=torch.float32)
+    if mask is None:
+        out = paged_attention(q_bshd, key_cache_q8, value_cache, bt.contiguous(), sl.contiguous(), qsl,
+                              Sq, max_kv, scale, q_abs_offset=q_abs_offset,
+                              causal=q_abs_offset is not None, out_dtype=torch.float32)
+        return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
+    # materialised mask: the tiled kernel over the same planar Q8 planes
+    mk, mbs, mrs, mcols = _mask_args(mask, B, Sq, q_abs_offset)
+    q_bshd = q_bshd.contiguous()
+    sl = sl.contiguous()
+    _check(q_bshd.dtype in _DT, "q must be fp32, fp16 or bf16")
+    bs, Hkv, cbs, chs = _plane_info(key_cache_q8, value_cache)
+    _check(Hq % Hkv == 0, f"heads_q={Hq} must be divisible by heads_kv={Hkv}")
+    out = torch.empty((B * Sq, Hq, D), dtype=torch.float32, device=q.device)
+    bt = bt.contiguous()
+    err = _load().gfx906_fa_amd_paged_attention_tiled(
+        _ptr(q_bshd), _DT[q_bshd.dtype], q_bshd.stride(0), q_bshd.stride(1), _ptr(key_cache_q8),
+        _ptr(value_cache), 0, cbs, chs, cbs, chs, _ptr(bt), bt.stride(0), _ptr(sl),
+        _ptr(qsl), None, 0, _ptr(mk), mbs, mrs, mcols, B, B * Sq, Hq, Hkv, D, bs, Sq, float(scale),
+        _ptr(out), out.stride(0), out.stride(1), _stream(q.device))
+    _ok(err, "gfx906_fa_amd_paged_attention_tiled")
     return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
 
 

@@ -205,22 +205,33 @@ hipError_t gfx906_fa_amd_pack_flat_kv(const uint8_t *k_aos, const void *v_f16,
                                       uint8_t *k_planar, void *v_planar, int rows, int Skv,
                                       int head_size, hipStream_t stream);
 
-/* (7) Paged attention with a planar Q8 K plane and a planar fp16 V plane
- *     (layout of (6)), separate K / V page and kv-head strides (bytes).
- *     Semantics as (5): dequantized K, exact fp16 V, fp32 softmax; every
- *     sequence runs through the tiled (prefill) kernel, no workspace.  With
- *     (6) and block_size = Skv_pad this is the contiguous attention of
- *     gfx906_fa_launch (extension/gfx906_fa_launcher.cu:53-209): kv_max maps
- *     to seq_lens, q_abs_offset to the inline causal bound.
+/* (7) Tiled paged attention with a choice of V plane and an optional
+ *     additive mask; every sequence runs through the tiled (prefill) kernel,
+ *     no workspace, fp32 output.
+ *       v_format 0: planar Q8 V (as (5)); 1: planar fp16 V (layout of (6)).
+ *       K / V page and kv-head strides in bytes, given separately.
+ *       mask: NULL, or fp16 [num_seqs][n_q][mask_cols] with element strides
+ *       mask_batch_stride / mask_row_stride: score(j, k) += mask[s][j][k]
+ *       (natural-log units, added after the softmax scale as
+ *       kernel/fattn-q8.cuh:643-644 does); keys k >= mask_cols add 0.
+ *     Semantics otherwise as (5): dequantized K, exact fp16 (format 1) or
+ *     dequantized Q8 (format 0) V, fp32 softmax, kv cutoff seq_lens[s],
+ *     causal bound q_abs_offset (or seq_lens - n_q) when causal != 0.
+ *     With (6), block_size = Skv_pad and one page per sequence this is the
+ *     contiguous attention of gfx906_fa_launch
+ *     (extension/gfx906_fa_launcher.cu:53-209); with v_format 0 it is the
+ *     masked form of gfx906_fa_launch_paged
+ *     (extension/gfx906_fa_launcher.cu:222-352).
  */
-hipError_t gfx906_fa_amd_paged_attention_f16v(
+hipError_t gfx906_fa_amd_paged_attention_tiled(
     const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
-    const uint8_t *k_cache, const void *v_cache_f16, int64_t k_block_stride,
+    const uint8_t *k_cache, const void *v_cache, int v_format, int64_t k_block_stride,
     int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride,
     const int32_t *block_table, int64_t block_table_stride, const int32_t *seq_lens,
-    const int32_t *query_start_loc, const int32_t *q_abs_offset, int causal, int num_seqs,
-    int num_tokens, int num_heads, int num_kv_heads, int head_size, int block_size,
-    int max_query_len, float scale, void *out, int out_dtype, int64_t out_token_stride,
+    const int32_t *query_start_loc, const int32_t *q_abs_offset, int causal,
+    const void *mask, int64_t mask_batch_stride, int64_t mask_row_stride, int mask_cols,
+    int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
+    int block_size, int max_query_len, float scale, float *out, int64_t out_token_stride,
     int64_t out_head_stride, hipStream_t stream);
 
 #ifdef __cplusplus

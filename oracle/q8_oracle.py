@@ -397,7 +397,7 @@ def paged_attention_ref(query: np.ndarray, k_hat: np.ndarray, v_hat: np.ndarray,
 
 
 def flat_attention_ref(q: np.ndarray, k_aos: np.ndarray, v: np.ndarray, scale: float,
-                       kv_max=None, q_abs_offset=None) -> np.ndarray:
+                       kv_max=None, q_abs_offset=None, mask=None) -> np.ndarray:
     """Contiguous attention of the op module's ``forward``
     (``extension/gfx906_fa.cpp:120-265``; kernel ``kernel/fattn-q8.cuh:835-1087``)
     over dequantized K and exact fp16 V, float64 softmax.
@@ -407,7 +407,8 @@ def flat_attention_ref(q: np.ndarray, k_aos: np.ndarray, v: np.ndarray, scale: f
     Skv keys without kv_max; ``extension/gfx906_fa.cpp:189-212``) and, with
     q_abs_offset, k <= q_abs_offset[b] + j (``kernel/fattn-q8.cuh:646-653``).
     q-head h reads kv-head h // (Hq/Hkv) (``kernel/fattn-q8.cuh:898-901``).
-    A row with no visible key outputs 0."""
+    mask [B, Sq, >= Skv]: added to the scaled scores
+    (``kernel/fattn-q8.cuh:643-644``).  A row with no visible key outputs 0."""
     B, Hq, Sq, D = q.shape
     Hkv, Skv = v.shape[1], v.shape[2]
     G = Hq // Hkv
@@ -423,10 +424,13 @@ def flat_attention_ref(q: np.ndarray, k_aos: np.ndarray, v: np.ndarray, scale: f
         for h in range(Hkv):
             qh = q[b, h * G:(h + 1) * G].astype(np.float64)           # [G, Sq, D]
             sc = np.einsum("gjd,kd->gjk", qh, K[b, h]) * scale
-            sc = np.where(vis[None], sc, -np.inf)
+            if mask is not None:
+                sc = sc + np.asarray(mask[b], dtype=np.float64)[None, :, :Skv]
+            vis2 = vis[None] & (sc > -np.inf)
+            sc = np.where(vis2, sc, -np.inf)
             m = np.max(sc, axis=-1, keepdims=True)
             m = np.where(np.isfinite(m), m, 0.0)
-            p = np.where(vis[None], np.exp(sc - m), 0.0)
+            p = np.where(vis2, np.exp(sc - m), 0.0)
             l = p.sum(-1, keepdims=True)
             o = np.einsum("gjk,kd->gjd", p, V[b, h])
             out[b, h * G:(h + 1) * G] = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)

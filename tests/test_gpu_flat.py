@@ -88,11 +88,68 @@ def test_forward_flat(case):
     assert_close(out.cpu().numpy(), ref)
 
 
-def test_forward_flat_rejects_mask_and_bad_dims():
+def test_forward_flat_rejects_bad_arguments():
+    """The reference binding's checks (extension/gfx906_fa.cpp:131-227)."""
     need_gpu()
     q, kq, v = _inputs(3, 1, 2, 1, 4, 32)
     args = (torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV), torch.from_numpy(v).to(DEV), 0.1)
-    with pytest.raises(RuntimeError, match="mask"):
-        gfx906_fa.forward(*args, mask=torch.zeros((1, 4, 32), dtype=torch.float16, device=DEV))
+    with pytest.raises(RuntimeError, match="mask must be fp16"):
+        gfx906_fa.forward(*args, mask=torch.zeros((1, 4, 32), dtype=torch.float32, device=DEV))
+    with pytest.raises(RuntimeError, match="mask.size"):
+        gfx906_fa.forward(*args, mask=torch.zeros((1, 4, 16), dtype=torch.float16, device=DEV))
     with pytest.raises(RuntimeError, match="fp32"):
         gfx906_fa.forward(args[0].half(), *args[1:])
+    with pytest.raises(RuntimeError, match="k_q8 last dim"):
+        gfx906_fa.forward(args[0], args[1][..., :100].contiguous(), *args[2:])
+
+
+def test_forward_flat_mask():
+    """Materialised fp16 mask: a causal 0/-inf mask and a dense additive one."""
+    need_gpu()
+    announce("forward mask B=2 Hq=8 Hkv=2 Sq=40 Skv=100")
+    B, Hq, Hkv, Sq, Skv = 2, 8, 2, 40, 100
+    q, kq, v = _inputs(77, B, Hq, Hkv, Sq, Skv)
+    rng = np.random.default_rng(78)
+    Skv_pad = 128
+    pos = np.arange(Skv_pad)
+    qa = np.array([60, 0], np.int32)
+    causal = np.where(pos[None, None, :] <= qa[:, None, None] + np.arange(Sq)[None, :, None], 0.0, -np.inf)
+    for m in (causal.astype(np.float16), rng.standard_normal((B, Sq, Skv_pad)).astype(np.float16)):
+        out = gfx906_fa.forward(torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV),
+                                torch.from_numpy(v).to(DEV), 0.09, mask=torch.from_numpy(m).to(DEV))
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), O.flat_attention_ref(q, kq, v, 0.09, mask=m))
+    with pytest.raises(RuntimeError, match="mutually exclusive"):
+        gfx906_fa.forward(torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV), torch.from_numpy(v).to(DEV),
+                          0.09, mask=torch.from_numpy(m).to(DEV), q_abs_offset=torch.from_numpy(qa).to(DEV))
+
+
+def test_forward_paged_direct_mask():
+    """forward_paged_direct with a dense additive mask over the planar Q8 cache
+    (the paged path's dequantized V) against the flat oracle on the same values."""
+    need_gpu()
+    announce("forward_paged_direct mask")
+    B, Hq, Hkv, Sq, Skv, bs = 2, 6, 1, 20, 70, 16
+    rng = np.random.default_rng(79)
+    k = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
+    q = rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32)
+    nbs = (Skv + bs - 1) // bs
+    bt = rng.permutation(B * nbs).astype(np.int32).reshape(B, nbs)
+    cache = gfx906_fa.new_kv_cache(B * nbs, bs, Hkv, device=DEV)
+    pos = np.arange(Skv)
+    for b in range(B):
+        slots = torch.from_numpy((bt[b, pos // bs].astype(np.int64) * bs + pos % bs)).to(DEV)
+        gfx906_fa.reshape_and_cache_q8_kv(torch.from_numpy(k[b].transpose(1, 0, 2).copy()).to(DEV),
+                                          torch.from_numpy(v[b].transpose(1, 0, 2).copy()).to(DEV),
+                                          slots, cache[:, 0], cache[:, 1])
+    m = rng.standard_normal((B, Sq, 80)).astype(np.float16)
+    sl = np.array([70, 45], np.int32)
+    out = gfx906_fa.forward_paged_direct(torch.from_numpy(q).to(DEV), cache[:, 0], cache[:, 1],
+                                         torch.from_numpy(bt).to(DEV), torch.from_numpy(sl).to(DEV), 0.1,
+                                         mask=torch.from_numpy(m).to(DEV))
+    torch.cuda.synchronize()
+    kq = O.quantize_q8_0_rows(k)
+    vh = O.dequantize_q8_0_rows(O.quantize_q8_0_rows(v), 128)
+    ref = O.flat_attention_ref(q, kq, vh, 0.1, kv_max=sl, mask=m)
+    assert_close(out.cpu().numpy(), ref)

@@ -275,3 +275,24 @@ def test_planar_v16_layout_bijection():
     T, i = lane // 16, lane % 16
     got = sorted(int(O.planar_v16_pos(4 * T + s, i + 16 * (4 * hf + mm))) for s in range(4) for mm in range(4))
     assert got == list(range(2048 * hf + 32 * lane, 2048 * hf + 32 * lane + 32, 2))
+
+
+def test_flat_attention_oracle_mask():
+    """An fp16 causal mask (0 / -inf) equals the inline causal bound; an
+    additive mask matches SDPA with a float mask."""
+    rng = np.random.default_rng(11)
+    q, kq, v = _flat_case(rng, 2, 4, 2, 6, 30)
+    qa = np.array([24, 10], np.int32)
+    pos = np.arange(32)
+    causal = np.where(pos[None, None, :] <= qa[:, None, None] + np.arange(6)[None, :, None], 0.0, -np.inf)
+    a = O.flat_attention_ref(q, kq, v, 0.1, mask=causal.astype(np.float16))
+    b = O.flat_attention_ref(q, kq, v, 0.1, q_abs_offset=qa)
+    assert np.max(np.abs(a - b)) < 1e-12
+    add = rng.standard_normal((2, 6, 32)).astype(np.float16)
+    got = O.flat_attention_ref(q, kq, v, 0.1, mask=add)
+    K = torch.from_numpy(O.dequantize_q8_0_rows(kq, 128)).double().repeat_interleave(2, dim=1)
+    V = torch.from_numpy(v.astype(np.float64)).repeat_interleave(2, dim=1)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q).double(), K, V, attn_mask=torch.from_numpy(add[:, None, :, :30].astype(np.float64)),
+        scale=0.1)
+    assert np.max(np.abs(got - ref.numpy())) < 1e-10
