@@ -65,13 +65,30 @@ class Gfx906FAMetadata:
     common_prefix_len: int = 0
 
 
+def workspace_upper_bound(max_num_seqs: int) -> int:
+    """Attention workspace that covers every batch of up to max_num_seqs
+    sequences (32-row decode tiles, the larger slot size; the workspace does
+    not depend on context lengths)."""
+    return gfx906_fa.workspace_size(max_num_seqs, max_num_seqs, 32, 1, 1, 1)
+
+
 class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
-    _cudagraph_support: ClassVar[AttentionCGSupport] = AttentionCGSupport.NEVER
+    # Graph-capturable for batches of one query length (decode, speculative
+    # verify): the kernels read every per-step value from device memory, size
+    # their grids from fixed shapes only, allocate nothing and record no
+    # memset (the reference is NEVER, extension/gfx906_fa_backend.py:75).
+    _cudagraph_support: ClassVar[AttentionCGSupport] = AttentionCGSupport.UNIFORM_BATCH
 
     def __init__(self, kv_cache_spec: AttentionSpec, layer_names: list[str],
                  vllm_config: VllmConfig, device: torch.device):
         super().__init__(kv_cache_spec, layer_names, vllm_config, device)
         self.block_size = kv_cache_spec.block_size
+        # reserve the shared workspace before any capture, so forward() never
+        # allocates inside a graph
+        sched = getattr(vllm_config, "scheduler_config", None)
+        max_seqs = getattr(sched, "max_num_seqs", None)
+        if isinstance(max_seqs, int) and max_seqs > 0 and torch.device(device).type == "cuda":
+            Gfx906FAImpl.reserve_workspace(workspace_upper_bound(max_seqs), torch.device(device))
 
     def build_for_cudagraph_capture(self, common_attn_metadata: CommonAttentionMetadata
                                     ) -> Gfx906FAMetadata:
@@ -215,12 +232,21 @@ class Gfx906FAImpl(AttentionImpl):
         return False
 
     @classmethod
-    def _get_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor | None:
+    def reserve_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor:
+        """Grow the shared workspace to at least nbytes (never shrinks)."""
         ws = cls._workspace
         if ws is None or ws.numel() < nbytes or ws.device != device:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"GFX906_FA: attention workspace of {nbytes} bytes needed inside graph "
+                    "capture; reserve it before capturing (Gfx906FAImpl.reserve_workspace)")
             cls._workspace = None
-            cls._workspace = gfx906_fa.new_workspace(nbytes, device)
+            cls._workspace = gfx906_fa.new_workspace(max(nbytes, 0 if ws is None else ws.numel()), device)
         return cls._workspace
+
+    @classmethod
+    def _get_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor:
+        return cls.reserve_workspace(nbytes, device)
 
     def do_kv_cache_update(self, layer: AttentionLayer, key: torch.Tensor, value: torch.Tensor,
                            kv_cache: torch.Tensor, slot_mapping: torch.Tensor):

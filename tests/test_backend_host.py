@@ -84,3 +84,19 @@ def test_q8_planes_inside_vllm_pages():
     planar = torch.zeros((NB, 2, Hkv, 2176), dtype=torch.uint8)
     k2, v2 = q8_planes(planar, Hkv, 128)
     assert k2.data_ptr() == planar.data_ptr()
+
+
+def test_graph_support_and_workspace_bound():
+    """The builder declares graph support for uniform batches; the workspace
+    it reserves up front covers every batch of up to max_num_seqs sequences,
+    whatever the heads, query length or context."""
+    import gfx906_fa
+    from gfx906_fa_backend import Gfx906FAMetadataBuilder, workspace_upper_bound
+    from vllm.v1.attention.backend import AttentionCGSupport
+    assert Gfx906FAMetadataBuilder._cudagraph_support == AttentionCGSupport.UNIFORM_BATCH
+    for max_seqs in (1, 7, 256):
+        bound = workspace_upper_bound(max_seqs)
+        for n in {1, max_seqs // 2 or 1, max_seqs}:
+            for Hq, Hkv in ((48, 8), (6, 1), (32, 32)):
+                for mq in (1, 4, 5, 16, 2048):
+                    assert gfx906_fa.workspace_size(n, n * mq, Hq, Hkv, mq, 1 << 17) <= bound

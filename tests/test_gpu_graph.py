@@ -1,0 +1,93 @@
+"""GPU: a decode step (quantize-write of the new tokens + paged attention)
+captured once in a HIP graph and replayed with new sequence lengths, block
+tables and token values written in place.  Every replay is checked bit for
+bit against the same step run eagerly (with the program's own eager work and
+synchronisations between replays), and one replay against the oracle.  The
+attention path allocates nothing inside the C ABI, records no memset, and
+sizes its grids from host-fixed shapes only (CU count, num_seqs, heads,
+max_query_len), so the graph stays valid while the device-side metadata
+changes."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import gfx906_fa
+from gpu_common import announce, assert_close, need_gpu
+from oracle import q8_oracle as O
+
+DEV = "cuda"
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("heads,q_len", [((48, 8), 1), ((6, 1), 5)])
+def test_decode_step_graph_replay(heads, q_len):
+    need_gpu()
+    Hq, Hkv = heads
+    announce(f"graph replay heads={heads} q_len={q_len}")
+    B, bs, max_blocks = 8, 16, 48
+    NB = B * max_blocks
+    T = B * q_len
+    scale = 1.0 / math.sqrt(128)
+    rng = np.random.default_rng(5)
+    cache = gfx906_fa.new_kv_cache(NB, bs, Hkv, device=DEV)
+    kp, vp = cache[:, 0], cache[:, 1]
+    # fill every page once (eager) so any block table reads written data
+    allk = torch.from_numpy(rng.standard_normal((NB * bs, Hkv, 128)).astype(np.float16)).to(DEV)
+    allv = torch.from_numpy(rng.standard_normal((NB * bs, Hkv, 128)).astype(np.float16)).to(DEV)
+    gfx906_fa.reshape_and_cache_q8_kv(allk, allv, torch.arange(NB * bs, dtype=torch.int64, device=DEV), kp, vp)
+    # static graph inputs / outputs
+    q = torch.empty((T, Hq, 128), dtype=torch.float16, device=DEV)
+    k_new = torch.empty((T, Hkv, 128), dtype=torch.float16, device=DEV)
+    v_new = torch.empty_like(k_new)
+    slots = torch.empty(T, dtype=torch.int64, device=DEV)
+    bt = torch.empty((B, max_blocks), dtype=torch.int32, device=DEV)
+    sl = torch.empty(B, dtype=torch.int32, device=DEV)
+    qsl = torch.arange(0, (B + 1) * q_len, q_len, dtype=torch.int32, device=DEV)
+    out = torch.empty((T, Hq, 128), dtype=torch.float16, device=DEV)
+    ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(B, T, Hq, Hkv, q_len, max_blocks * bs), DEV)
+
+    def load_inputs(seed):
+        r = np.random.default_rng(seed)
+        lens = r.integers(q_len, max_blocks * bs + 1, B).astype(np.int32)
+        table = r.permutation(NB)[: B * max_blocks].astype(np.int32).reshape(B, max_blocks)
+        pos = (lens[:, None] - q_len + np.arange(q_len)[None, :]).reshape(-1)
+        rows = np.repeat(np.arange(B), q_len)
+        sm = table[rows, pos // bs].astype(np.int64) * bs + pos % bs
+        sl.copy_(torch.from_numpy(lens))
+        bt.copy_(torch.from_numpy(table))
+        slots.copy_(torch.from_numpy(sm))
+        q.copy_(torch.from_numpy(r.standard_normal((T, Hq, 128)).astype(np.float16)))
+        k_new.copy_(torch.from_numpy(r.standard_normal((T, Hkv, 128)).astype(np.float16)))
+        v_new.copy_(torch.from_numpy(r.standard_normal((T, Hkv, 128)).astype(np.float16)))
+        return lens, table
+
+    def step():
+        gfx906_fa.reshape_and_cache_q8_kv(k_new, v_new, slots, kp, vp)
+        gfx906_fa.paged_attention(q, kp, vp, bt, sl, qsl, q_len, max_blocks * bs, scale, out=out, workspace=ws)
+
+    load_inputs(100)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for it in range(4):
+        lens, table = load_inputs(200 + it)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        step()  # eager, same inputs (the cache write is idempotent)
+        torch.cuda.synchronize()
+        assert torch.equal(got, out), f"replay {it} differs from the eager step"
+        if it == 3:
+            kh, vh = O.planar_dequant(cache.cpu().numpy())
+            ref = O.paged_attention_ref(q.float().cpu().numpy(), kh, vh, table, lens,
+                                        qsl.cpu().numpy(), scale)
+            assert_close(got.float().cpu().numpy(), ref)
