@@ -665,6 +665,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
+#ifndef GFA_PF_PRIO
+#define GFA_PF_PRIO 0  // s_setprio 1 around the QK (bit 0) / PV (bit 1) MFMA issue
+#endif
 #ifndef GFA_PF_SCHED
 #define GFA_PF_SCHED 0  // VALU instructions per QK MFMA slot (0: compiler's schedule)
 #endif
@@ -911,6 +914,9 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         }
 
         // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile
+#if GFA_PF_PRIO & 1
+        __builtin_amdgcn_s_setprio(1);
+#endif
         float16v_t sacc[PF_NST];
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
@@ -921,6 +927,9 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
+#if GFA_PF_PRIO & 1
+        __builtin_amdgcn_s_setprio(0);
+#endif
 #if GFA_PF_SCHED
         // interleave the next tile's dequant (VALU + LDS stores) with the QK
         // MFMAs and their operand reads
@@ -979,6 +988,9 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
             for (int e = 0; e < 16; ++e) cneg[e] = -m_use;
         }
         const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
+#if GFA_PF_PRIO & 2
+        __builtin_amdgcn_s_setprio(1);
+#endif
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
 #pragma unroll
@@ -1000,6 +1012,9 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 }
             }
         }
+#if GFA_PF_PRIO & 2
+        __builtin_amdgcn_s_setprio(0);
+#endif
         __syncthreads();
     };
     using Even = std::integral_constant<bool, false>;
