@@ -253,3 +253,24 @@ def test_full_size_mixed_cfg4():
     qsl = b.qsl
     sample = [0, 2047, 2048 + 5, 3 * 2048 + 2047] + [int(qsl[4 + i]) for i in (0, 17, 59)]
     _run_and_check(b, rows=sample)
+
+
+def test_decode_many_short_sequences():
+    """700 decode sequences of 1..400 tokens (several per workgroup range,
+    many segments shorter than a sub-page) plus a few long ones that split."""
+    need_gpu()
+    rng = np.random.default_rng(21)
+    sl = rng.integers(1, 401, 700).tolist() + [9000, 17, 30000]
+    b = W.build_batch(sl, [1] * len(sl), 16, 4, seed=21)
+    _run_and_check(b)
+
+
+def test_mixed_many_chunks():
+    """Varlen mix of 40 prefill chunks (n_q 2..300, causal within each, prior
+    context 0..3000) and 100 decode sequences in one call."""
+    need_gpu()
+    rng = np.random.default_rng(22)
+    ql = rng.integers(2, 301, 40).tolist() + [1] * 100
+    sl = [q + int(c) for q, c in zip(ql, rng.integers(0, 3001, len(ql)))]
+    b = W.build_batch(sl, ql, 12, 3, seed=22)
+    _run_and_check(b)
