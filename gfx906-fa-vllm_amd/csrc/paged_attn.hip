@@ -665,12 +665,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
-#ifndef GFA_PF_PRIO
-#define GFA_PF_PRIO 0  // s_setprio 1 around the QK (bit 0) / PV (bit 1) MFMA issue
-#endif
-#ifndef GFA_PF_SCHED
-#define GFA_PF_SCHED 0  // VALU instructions per QK MFMA slot (0: compiler's schedule)
-#endif
 constexpr int PF_WAVES = 8;
 constexpr int PF_ROWS = 32 * PF_WAVES;
 #ifndef GFA_PF_TK
@@ -914,9 +908,6 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         }
 
         // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile
-#if GFA_PF_PRIO & 1
-        __builtin_amdgcn_s_setprio(1);
-#endif
         float16v_t sacc[PF_NST];
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
@@ -927,20 +918,6 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
-#if GFA_PF_PRIO & 1
-        __builtin_amdgcn_s_setprio(0);
-#endif
-#if GFA_PF_SCHED
-        // interleave the next tile's dequant (VALU + LDS stores) with the QK
-        // MFMAs and their operand reads
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x002, GFA_PF_SCHED, 0);  // VALU
-            if (i % 3 == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-        }
-#endif
         const int kbase_t = PF_TK * kt;
         if constexpr (MASK) {  // S' += mask[s][j][key] (natural log units -> log2)
             const uint16_t *mrow = p.mask + (int64_t)s * p.mask_bs + (int64_t)j * p.mask_rs;
@@ -988,9 +965,6 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
             for (int e = 0; e < 16; ++e) cneg[e] = -m_use;
         }
         const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
-#if GFA_PF_PRIO & 2
-        __builtin_amdgcn_s_setprio(1);
-#endif
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
 #pragma unroll
@@ -1012,9 +986,6 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 }
             }
         }
-#if GFA_PF_PRIO & 2
-        __builtin_amdgcn_s_setprio(0);
-#endif
         __syncthreads();
     };
     using Even = std::integral_constant<bool, false>;
@@ -1133,7 +1104,7 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int nu
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
-        const int tiles = (rows + 32 * PF_WAVES - 1) / (32 * PF_WAVES);
+        const int tiles = (rows + PF_ROWS - 1) / PF_ROWS;
         attn_prefill_kernel<QDT, ODT, false, false><<<dim3(tiles * num_kv_heads, num_seqs), 64 * PF_WAVES, 0, stream>>>(p);
     }
     return hipGetLastError();
