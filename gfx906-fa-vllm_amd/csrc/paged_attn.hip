@@ -1095,12 +1095,14 @@ template <int QDT, int ODT>
 hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int num_kv_heads,
                       int max_query_len, hipStream_t stream) {
     AttnParams p = p0;
+    // combine rows: a split segment has at most min(max_query_len * G, slot) rows
+    const int crow = max(1, min(max_query_len * p.G, pl.dec_rows_max));
     if (pl.dec_nrg == 1) {
         attn_decode_kernel<1, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, 16), 256, 0, stream>>>(p);
+        attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(p);
     } else {
         attn_decode_kernel<2, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, 32), 256, 0, stream>>>(p);
+        attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(p);
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
