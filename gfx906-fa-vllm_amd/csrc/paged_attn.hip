@@ -964,7 +964,11 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
 #pragma unroll
             for (int e = 0; e < 16; ++e) cneg[e] = -m_use;
         }
-        const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
+        // The row sum is accumulated with plain fp32 adds of the unrounded p
+        // (as the decode path does): v_dot2 runs on the matrix pipe and would
+        // serialise with the other wave's MFMAs, whereas adds, exps and
+        // conversions issue under them.
+        float tsum = 0.0f;
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
 #pragma unroll
@@ -975,7 +979,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                     const float p0 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + 2 * e]);
                     const float p1 = __builtin_amdgcn_exp2f(sacc[st][8 * sg + 2 * e + 1]);
                     pk.h[e] = half2_t{(half_t)p0, (half_t)p1};
-                    l_run = __builtin_amdgcn_fdot2(pk.h[e], ones, l_run, false);
+                    tsum += p0 + p1;
                 }
                 const half8_t pb = __builtin_bit_cast(half8_t, pk);
 #pragma unroll
@@ -986,6 +990,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
                 }
             }
         }
+        l_run += tsum;
         __syncthreads();
     };
     using Even = std::integral_constant<bool, false>;
