@@ -854,6 +854,11 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     const uint8_t *vplane = p.vc + (int64_t)h * p.vchs;
     constexpr int VSUB = VF16 ? 4096 : SUBPAGE_BYTES;  // V bytes per 16-token sub-page
     int pw0 = 0, pw1 = 0, cbase = 0;
+    // Waits for a window load right where it is issued (once per 64 tiles):
+    // a window register still pending inside the loop would make every
+    // v_readlane of it wait for all loads in flight (vmcnt counts in order),
+    // the K/V fetches of the previous step included.
+    auto ready = [](int &v) { asm volatile("" : "+v"(v)); };
     struct PfRawT {
         PfRaw h[PF_NSP == 8 ? 2 : 1];
     };
@@ -1002,6 +1007,8 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     if (ntk > 0) {
         pw0 = load_pg(0);
         pw1 = ntk > 64 ? load_pg(1) : 0;
+        ready(pw0);
+        ready(pw1);
         fetch(r0, 0);
         if (ntk > 1) {
             fetch(r1, 1);
@@ -1021,6 +1028,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
             cbase += 64;
             pw0 = pw1;
             pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
+            ready(pw1);
         }
     }
     // the last 1-3 tiles (uniform)
