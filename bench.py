@@ -1,6 +1,7 @@
 """Benchmark of the Q8_0 paged-attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-prefill]
+    python bench.py --workload {cfg3,cfg4,cfg5,cfg5-48}   (one other configuration)
 
 Headline (``value``): batched decode, cfg2 of the benchmark definition - 32 sequences with
 contexts U[2048, 16384], 48 query / 8 KV heads, head_dim 128, fp16 Q, Q8_0
@@ -21,6 +22,13 @@ Also reported on the same JSON line:
   cpu_baseline  - the reference's PyTorch CPU path (paged gather + dequantize
                   + fp32 SDPA, oracle/cpu_baseline.py) on whole cfg2
                   sequences, repeated for a ~10 s budget, same GB/s accounting.
+
+--workload times the attention pass of another configuration of the benchmark
+definition instead (the line's roofline is that workload's dominant kernel):
+  cfg3     32K causal prefill (MFMA-bound: TFLOP/s)
+  cfg4     mixed chunked prefill + decode; the prefill chunks and the decode
+           sequences are also timed as batches of their own (``parts``)
+  cfg5     speculative verify, 6/1 heads (HBM-bound: GB/s); cfg5-48: 48/8 heads
 """
 from __future__ import annotations
 
@@ -82,6 +90,79 @@ def timed(fn, steps: int, warmup: int):
     return s.elapsed_time(e) / steps
 
 
+def _attn_fn(b, out, ws):
+    import gfx906_fa
+    kp, vp = b.planes()
+
+    def f():
+        gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t,
+                                  b.max_query_len, b.max_seq_len, b.scale, out=out, workspace=ws)
+    return f
+
+
+def other_workload(args, dev) -> dict:
+    """One attention pass of cfg3 / cfg4 / cfg5 (inputs resident in HBM),
+    timed with HIP events on the launch stream."""
+    import torch
+
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+
+    name = "cfg5" if args.workload.startswith("cfg5") else args.workload
+    heads = (48, 8) if args.workload == "cfg5-48" else None
+    b = W.build_cfg(name, device=dev, heads=heads)
+    odt = torch.bfloat16 if b.dtype == "bf16" else torch.float16
+
+    def new_out(bb):
+        return torch.empty((bb.num_tokens, bb.Hq, bb.D), dtype=odt, device=dev)
+
+    def new_ws(bb):
+        return gfx906_fa.new_workspace(gfx906_fa.workspace_size(
+            bb.num_seqs, bb.num_tokens, bb.Hq, bb.Hkv, bb.max_query_len, bb.max_seq_len), dev)
+
+    steps = args.steps if name == "cfg5" else max(3, min(10, args.steps // 5))
+    ms = timed(_attn_fn(b, new_out(b), new_ws(b)), steps, max(2, min(args.warmup, 10)))
+    fl, hb = b.flops(), b.hbm_bytes(out_bytes_per_elem=2)
+    gbs, tfs = hb / (ms * 1e-3) / 1e9, fl / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "Q8 paged decode HBM GB/s (% of peak); causal prefill attn TFLOP/s @32K",
+        "n_gpus": 1, "steps": steps, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": b.dtype, "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {W.CONFIGS[name]}", "num_seqs": b.num_seqs,
+                   "num_tokens": b.num_tokens, "heads": f"{b.Hq}/{b.Hkv}", "total_context": int(b.seq_lens.sum()),
+                   "algorithmic_bytes": hb, "flop": fl, "parallelism": "single GPU"},
+    }
+    if name == "cfg5":
+        res.update({"value": round(gbs, 1), "unit": "GB/s"})
+        res["roofline"] = {"bound": "hbm", "kernel": "attn_decode_kernel+attn_combine_kernel",
+                           "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(ms * 1e3, 2)}
+    elif name == "cfg3":
+        res.update({"value": round(tfs, 2), "unit": "TFLOP/s"})
+        res["roofline"] = {"bound": "mfma", "kernel": "attn_prefill_kernel", "achieved": round(tfs, 2),
+                           "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_PEAK_TFLOPS, 4),
+                           "traffic": None, "avg_us": round(ms * 1e3, 2)}
+    else:  # cfg4: both bounds; the parts timed as batches of their own
+        npf = int((b.q_lens > 1).sum())
+        pf, dc = W.sub_batch(b, 0, npf), W.sub_batch(b, npf, b.num_seqs)
+        ms_pf = timed(_attn_fn(pf, new_out(pf), new_ws(pf)), steps, 2)
+        ms_dc = timed(_attn_fn(dc, new_out(dc), new_ws(dc)), max(steps, 20), 3)
+        t_roof = pf.flops() / (MFMA_PEAK_TFLOPS * 1e12) + dc.hbm_bytes(2) / (HBM_PEAK_GBS * 1e9)
+        res.update({"value": round(t_roof / (ms * 1e-3), 4), "unit": "fraction of the summed roofline time"})
+        res["roofline"] = {"bound": "mfma+hbm", "kernel": "attn_prefill_kernel+attn_decode_kernel",
+                           "achieved": round(t_roof * 1e3, 4), "peak": round(ms, 4), "unit": "ms (roofline / measured)",
+                           "frac": round(t_roof / (ms * 1e-3), 4), "traffic": None}
+        res["parts"] = {
+            "prefill_chunks": {"ms": round(ms_pf, 4), "flop": pf.flops(),
+                               "tflops": round(pf.flops() / (ms_pf * 1e-3) / 1e12, 2),
+                               "frac_of_mfma_peak": round(pf.flops() / (ms_pf * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
+            "decode_seqs": {"ms": round(ms_dc, 4), "bytes": dc.hbm_bytes(2),
+                            "gbs": round(dc.hbm_bytes(2) / (ms_dc * 1e-3) / 1e9, 1),
+                            "frac_of_hbm_peak": round(dc.hbm_bytes(2) / (ms_dc * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        }
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +173,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (rocprof counter calibration)")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5", "cfg5-48"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -106,6 +188,9 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload != "cfg2":
+        print(json.dumps(other_workload(args, dev)), flush=True)
+        return 0
 
     # ---------------- cfg2 decode -----------------------------------------
     b = W.build_cfg("cfg2", device=dev)

@@ -157,6 +157,22 @@ def attention(b: Batch, out: Optional[torch.Tensor] = None, workspace=None,
                                      workspace=workspace, out_dtype=out_dtype)
 
 
+def sub_batch(b: Batch, s0: int, s1: int) -> Batch:
+    """The sequences [s0, s1) of a batch as a batch of their own over the same
+    KV cache (their query tokens are contiguous in the varlen layout)."""
+    qsl = b.qsl
+    t0, t1 = int(qsl[s0]), int(qsl[s1])
+    sb = Batch(Hq=b.Hq, Hkv=b.Hkv, D=b.D, block_size=b.block_size, seq_lens=b.seq_lens[s0:s1].copy(),
+               q_lens=b.q_lens[s0:s1].copy(), block_table_np=b.block_table_np[s0:s1].copy(),
+               num_blocks=b.num_blocks, dtype=b.dtype, scale=b.scale, device=b.device)
+    sb.query = b.query[t0:t1]
+    sb.kv_cache = b.kv_cache
+    sb.block_table = b.block_table[s0:s1].contiguous()
+    sb.seq_lens_t = b.seq_lens_t[s0:s1].contiguous()
+    sb.qsl_t = torch.from_numpy(sb.qsl).to(b.device)
+    return sb
+
+
 # ---------------------------------------------------------------------------
 # The benchmark configurations
 # ---------------------------------------------------------------------------
