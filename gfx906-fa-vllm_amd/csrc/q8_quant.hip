@@ -138,6 +138,117 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Planar K+V write, block per lane (D = 128).  One wave per (16 consecutive
+// tokens, kv-head): lane l takes token t0 + l%16 and Q8_0 block b = l/16, so
+// the 32 values of a block sit in one lane and amax needs no cross-lane
+// reduction; the per-element arithmetic is the closed form of
+// q8_quantize_pair.  Each lane writes its own slot (any slot mapping; slot <
+// 0 or a token past the end writes nothing):
+//   K ints : four 8-byte stores, kpos(tt, 32b + 8g) for g = 0..3
+//   V ints : 32 byte stores at vpos(tt, 32b + e)
+//   scales : one fp16 each (K at 2048 + (4tt+b)*2, V at 2048 + ((tt/4)*4+b)*8 + (tt%4)*2)
+// (tt = slot % 16 is the token's place in its sub-page.)  Needs the cache
+// bases and strides 8-byte aligned.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load_block32(const void *x, int64_t off, float (&v)[QK]) {
+    if constexpr (VEC && DT != GFA_DTYPE_F32) {
+        const u32x4 *p = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(x) + off);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 w = p[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t we = w[e];
+                if constexpr (DT == GFA_DTYPE_F16) {
+                    v[8 * c + 2 * e] = half_bits_to_f32(we & 0xFFFFu);
+                    v[8 * c + 2 * e + 1] = half_bits_to_f32(we >> 16);
+                } else {
+                    v[8 * c + 2 * e] = bf16_bits_to_f32(we & 0xFFFFu);
+                    v[8 * c + 2 * e + 1] = bf16_bits_to_f32(we >> 16);
+                }
+            }
+        }
+    } else if constexpr (VEC) {
+        const float4_t *p = reinterpret_cast<const float4_t *>(static_cast<const float *>(x) + off);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4_t w = p[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * c + e] = w[e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < QK; ++e) v[e] = load_as_f32<DT>(x, off + e);
+    }
+}
+
+// the Q8_0 closed form over one lane's 32 values (see q8_quantize_pair)
+__device__ __forceinline__ float quantize_block32(const float (&v)[QK], int8_t (&q)[QK]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < QK; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+    for (int e = 0; e < QK; ++e) {
+        int qi = (int)rintf(v[e] * id);
+        qi = qi < -128 ? -128 : (qi > 127 ? 127 : qi);
+        q[e] = (int8_t)qi;
+    }
+    return d;
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void q8_cache_write_kv_blk_kernel(
+    const void *__restrict__ key, const void *__restrict__ value,
+    const int64_t *__restrict__ slot_mapping, uint8_t *__restrict__ kc,
+    uint8_t *__restrict__ vc, int num_tokens, int num_kv_heads, int block_size,
+    int64_t kts, int64_t khs, int64_t vts, int64_t vhs, int64_t cbs, int64_t chs) {
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t grp = wave / num_kv_heads;
+    const int h = (int)(wave - grp * num_kv_heads);
+    const int64_t t = 16 * grp + (lane & 15);
+    const int b = lane >> 4;
+    if (t >= num_tokens) return;  // per lane: nothing below is shared
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) return;
+    const int64_t page = slot / block_size;
+    const int off = (int)(slot - page * block_size);
+    const int sp = off >> 4, tt = off & 15;
+    const int64_t base = page * cbs + (int64_t)h * chs + (int64_t)sp * SUBPAGE_BYTES;
+
+    float v[QK];
+    int8_t q[QK];
+    // K: four 8-byte runs (d = 32b + 8g .. +7) and the block scale
+    load_block32<DT, VEC>(key, t * kts + (int64_t)h * khs + QK * b, v);
+    float d = quantize_block32(v, q);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lo |= (uint32_t)(uint8_t)q[8 * g + e] << (8 * e);
+            hi |= (uint32_t)(uint8_t)q[8 * g + 4 + e] << (8 * e);
+        }
+        const int kpos = (b >> 1) * 1024 + (4 * tt + g) * 16 + (b & 1) * 8;
+        *reinterpret_cast<u32x2 *>(kc + base + kpos) = u32x2{lo, hi};
+    }
+    *reinterpret_cast<uint16_t *>(kc + base + SCALE_OFF + (4 * tt + b) * 2) = f32_to_half_bits(d);
+    // V: byte stores into the transposed (4 tokens per dword) layout
+    load_block32<DT, VEC>(value, t * vts + (int64_t)h * vhs + QK * b, v);
+    d = quantize_block32(v, q);
+    uint8_t *vrow = vc + base + (b >> 1) * 1024 + (tt >> 2) * 256 + (tt & 3);
+#pragma unroll
+    for (int e = 0; e < QK; ++e) {
+        const int m = 2 * b + (e >> 4);  // d / 16
+        vrow[(e & 15) * 16 + (m & 3) * 4] = (uint8_t)q[e];
+    }
+    *reinterpret_cast<uint16_t *>(vc + base + SCALE_OFF + ((tt >> 2) * 4 + b) * 8 + (tt & 3) * 2) =
+        f32_to_half_bits(d);
+}
+
 bool bad_dtype(int dt) { return dt != GFA_DTYPE_F32 && dt != GFA_DTYPE_F16 && dt != GFA_DTYPE_BF16; }
 
 }  // namespace
@@ -225,6 +336,34 @@ extern "C" hipError_t gfx906_fa_amd_cache_write_kv(
     const int esz = dtype == GFA_DTYPE_F32 ? 4 : 2;
     const bool vec = (((uintptr_t)key | (uintptr_t)value) % (2 * esz) == 0) && (kts % 2 == 0) &&
                      (khs % 2 == 0) && (vts % 2 == 0) && (vhs % 2 == 0);
+    if ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uint64_t)cbs | (uint64_t)chs) & 7u) == 0) {
+        // block per lane: vector loads need 16-byte aligned rows of 32 values
+        const bool vec16 = (((uintptr_t)key | (uintptr_t)value) % 16 == 0) &&
+                           ((kts * esz) % 16 == 0) && ((khs * esz) % 16 == 0) &&
+                           ((vts * esz) % 16 == 0) && ((vhs * esz) % 16 == 0);
+        const int64_t waves = (int64_t)((num_tokens + 15) / 16) * num_kv_heads;
+        const unsigned grid = (unsigned)((waves + 3) / 4);
+#define GFA_LAUNCH_BLK(DT, V)                                                                    \
+    q8_cache_write_kv_blk_kernel<DT, V><<<grid, 256, 0, stream>>>(key, value, slot_mapping,     \
+                                                                 k_cache, v_cache, num_tokens,   \
+                                                                 num_kv_heads, block_size, kts,  \
+                                                                 khs, vts, vhs, cbs, chs)
+        if (vec16) {
+            switch (dtype) {
+                case GFA_DTYPE_F32: GFA_LAUNCH_BLK(GFA_DTYPE_F32, true); break;
+                case GFA_DTYPE_F16: GFA_LAUNCH_BLK(GFA_DTYPE_F16, true); break;
+                default: GFA_LAUNCH_BLK(GFA_DTYPE_BF16, true); break;
+            }
+        } else {
+            switch (dtype) {
+                case GFA_DTYPE_F32: GFA_LAUNCH_BLK(GFA_DTYPE_F32, false); break;
+                case GFA_DTYPE_F16: GFA_LAUNCH_BLK(GFA_DTYPE_F16, false); break;
+                default: GFA_LAUNCH_BLK(GFA_DTYPE_BF16, false); break;
+            }
+        }
+#undef GFA_LAUNCH_BLK
+        return hipGetLastError();
+    }
     const int64_t waves = (int64_t)num_tokens * num_kv_heads;
     const unsigned grid = (unsigned)((waves + 3) / 4);
 #define GFA_LAUNCH_KV(DT, V)                                                                 \
