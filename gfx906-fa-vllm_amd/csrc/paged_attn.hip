@@ -72,11 +72,12 @@ struct AttnParams {
     int64_t *ws_hdr;      // decode plan published for the combine kernel: U, nwg
     int *ws_pre;          // per-sequence exclusive prefix of decode sub-pages
     int num_seqs, nwg;    // nwg: decode workgroups (the grid)
-    int dec_rows_max;     // rows handled by the decode kernel
+    int dec_rows_lo;      // a decode launch takes sequences with dec_rows_lo < n_q*G
+    int dec_rows_max;     //   <= dec_rows_max; the prefill kernel takes n_q*G > dec_rows_max
     // prefill work list (heaviest first) built by prefill_plan_kernel: item i
-    // is row tile pf_rt[i] of sequence pf_seq[i]; count in ws_hdr[2].
+    // is row tile pf_rt[i] of sequence pf_seq[i], *pf_count items.
     // nullptr: the prefill grid is (row tiles * Hkv, num_seqs) instead.
-    int *pf_seq, *pf_rt;
+    int *pf_seq, *pf_rt, *pf_count;
     int pf_items_max;
 };
 
@@ -401,7 +402,7 @@ __device__ __forceinline__ SegInfo seg_info(const AttnParams &p, int s) {
     si.sl = p.seq_lens[s];
     si.qa = p.q_abs ? p.q_abs[s] : si.sl - si.nq;
     si.kv_lim = p.causal ? min(si.sl, max(si.qa + si.nq, 0)) : si.sl;
-    const bool dec = si.nq > 0 && si.nq * p.G <= p.dec_rows_max;
+    const bool dec = si.nq > 0 && si.nq * p.G > p.dec_rows_lo && si.nq * p.G <= p.dec_rows_max;
     si.nsub = dec ? max((si.kv_lim + 15) >> 4, 1) : 0;
     return si;
 }
@@ -801,7 +802,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     int s, rt;
     if (p.pf_seq) {  // the sorted work list (uniform)
         const int item = blockIdx.x / Hkv;
-        if (item >= (int)p.ws_hdr[2]) return;
+        if (item >= p.pf_count[0]) return;
         s = p.pf_seq[item];
         rt = p.pf_rt[item];
     } else {         // row tiles last-first within each sequence
@@ -1181,19 +1182,35 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         p.pf_seq[pos] = sq;
         p.pf_rt[pos] = rt;
     }
-    if (tid == 0) p.ws_hdr[2] = n;
+    if (tid == 0) p.pf_count[0] = n;
 }
 
 // ---------------------------------------------------------------------------
 // Host-side plan.  Deterministic in the call's scalar arguments and the
 // device's CU count, so that workspace_size() and the launch agree.
-struct Plan {
-    int dec_nrg;        // 1 or 2 row groups per decode wave
-    int dec_rows_max;   // 16 or 32
+//
+// Decode work is split by packed rows per sequence into classes, each with
+// its own stream-K plan, workspace region and combine: n_q*G <= 16 runs the
+// one-row-group kernel (three waves per SIMD), 16 < n_q*G <= 32 the
+// two-row-group kernel (speculative verify).  A batch whose sequences all have
+// max_query_len tokens (num_tokens == num_seqs * max_query_len) needs at
+// most one class, and a uniform prefill batch none; a class launched alone
+// takes every row count up to its bound.  Sequences above the largest bound
+// go to the prefill kernel, which handles any row count.
+struct DecClass {
+    int nrg;            // row groups per decode wave (1 or 2)
+    int rows_lo, rows_hi;
     int nwg;            // decode workgroups (resident workgroups of the device)
+    size_t off_hdr, off_pre, off_ml, off_o;  // workspace layout
+};
+
+struct Plan {
+    DecClass dc[2];
+    int ndc;            // decode classes launched (0..2)
+    int dec_rows_max;   // largest decode row bound (0: every sequence is prefill)
     bool need_prefill;
     int pf_items_max;   // bound on prefill work items (0: no work list)
-    size_t off_hdr, off_pre, off_ml, off_o, off_items, bytes;  // workspace layout
+    size_t off_items, bytes;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1215,38 +1232,71 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     Plan pl;
     const int G = num_heads / num_kv_heads;
     const int max_rows = max_query_len * G;
-    pl.dec_nrg = (max_rows <= 16) ? 1 : 2;
-    pl.dec_rows_max = 16 * pl.dec_nrg;
+    const bool uniform = (int64_t)num_tokens == (int64_t)num_seqs * max_query_len;
+    pl.ndc = 0;
+    auto add = [&](int nrg, int lo, int hi) {
+        DecClass &c = pl.dc[pl.ndc++];
+        c.nrg = nrg;
+        c.rows_lo = lo;
+        c.rows_hi = hi;
+        c.nwg = device_cus() * 4 * (nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe) / DEC_NW;
+    };
+    if (max_rows <= 16) {
+        add(1, 0, 16);
+    } else if (uniform) {
+        if (max_rows <= 32) add(2, 0, 32);
+    } else {
+        if (G <= 16) add(1, 0, 16);
+        if (G <= 32) add(2, pl.ndc ? 16 : 0, 32);
+    }
+    pl.dec_rows_max = pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0;
     pl.need_prefill = max_rows > pl.dec_rows_max;
     // row tiles over all sequences <= sum ceil(n_q * G / 256) <= T*G/256 + B
     const int64_t items = ((int64_t)max(num_tokens, 0) * G + PF_ROWS - 1) / PF_ROWS + num_seqs;
     pl.pf_items_max = (pl.need_prefill && num_seqs <= PL_MAX_SEQS && items * num_kv_heads < INT32_MAX)
                           ? (int)items : 0;
-    const int wpe = pl.dec_nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe;
-    pl.nwg = device_cus() * 4 * wpe / DEC_NW;
-    const size_t rc = (size_t)pl.dec_rows_max;
-    pl.off_hdr = 0;
-    pl.off_pre = 256;
-    pl.off_ml = pl.off_pre + align256((size_t)num_seqs * sizeof(int));
-    pl.off_o = pl.off_ml + align256((size_t)2 * pl.nwg * rc * 2 * sizeof(float));
-    pl.off_items = pl.off_o + align256((size_t)2 * pl.nwg * rc * 128 * sizeof(float));
-    pl.bytes = pl.off_items + align256((size_t)2 * pl.pf_items_max * sizeof(int));
+    size_t off = 0;
+    for (int k = 0; k < pl.ndc; ++k) {
+        DecClass &c = pl.dc[k];
+        const size_t rc = (size_t)16 * c.nrg;
+        c.off_hdr = off;
+        c.off_pre = off + 256;
+        c.off_ml = c.off_pre + align256((size_t)num_seqs * sizeof(int));
+        c.off_o = c.off_ml + align256((size_t)2 * c.nwg * rc * 2 * sizeof(float));
+        off = c.off_o + align256((size_t)2 * c.nwg * rc * 128 * sizeof(float));
+    }
+    pl.off_items = off;
+    // work list: a 256-byte header (the item count), then the two item arrays
+    pl.bytes = max(pl.off_items + 256 + align256((size_t)2 * pl.pf_items_max * sizeof(int)), (size_t)256);
     return pl;
 }
 
 template <int QDT, int ODT>
-hipError_t launch_all(const AttnParams &p0, const Plan &pl, int num_seqs, int num_kv_heads,
+hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_seqs, int num_kv_heads,
                       int max_query_len, hipStream_t stream) {
     AttnParams p = p0;
+    p.dec_rows_lo = 0;
+    p.dec_rows_max = pl.dec_rows_max;
     if (pl.need_prefill && p.pf_seq) prefill_plan_kernel<<<1, PL_THREADS, 0, stream>>>(p);
-    // combine rows: a split segment has at most min(max_query_len * G, slot) rows
-    const int crow = max(1, min(max_query_len * p.G, pl.dec_rows_max));
-    if (pl.dec_nrg == 1) {
-        attn_decode_kernel<1, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(p);
-    } else {
-        attn_decode_kernel<2, QDT, ODT><<<pl.nwg, 64 * DEC_NW, 0, stream>>>(p);
-        attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(p);
+    for (int k = 0; k < pl.ndc; ++k) {
+        const DecClass &c = pl.dc[k];
+        AttnParams pd = p;
+        pd.dec_rows_lo = c.rows_lo;
+        pd.dec_rows_max = c.rows_hi;
+        pd.nwg = c.nwg;
+        pd.ws_hdr = reinterpret_cast<int64_t *>(ws + c.off_hdr);
+        pd.ws_pre = reinterpret_cast<int *>(ws + c.off_pre);
+        pd.ws_ml = reinterpret_cast<float *>(ws + c.off_ml);
+        pd.ws_o = reinterpret_cast<float *>(ws + c.off_o);
+        // combine rows: a split segment has at most min(max_query_len * G, slot) rows
+        const int crow = max(1, min(max_query_len * p.G, c.rows_hi));
+        if (c.nrg == 1) {
+            attn_decode_kernel<1, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
+            attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
+        } else {
+            attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
+            attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
+        }
     }
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
@@ -1333,22 +1383,23 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
     char *ws = static_cast<char *>(workspace);
-    p.ws_hdr = reinterpret_cast<int64_t *>(ws + pl.off_hdr);
-    p.ws_pre = reinterpret_cast<int *>(ws + pl.off_pre);
-    p.ws_ml = reinterpret_cast<float *>(ws + pl.off_ml);
-    p.ws_o = reinterpret_cast<float *>(ws + pl.off_o);
     p.num_seqs = num_seqs;
-    p.nwg = pl.nwg;
-    p.dec_rows_max = pl.dec_rows_max;
     p.pf_items_max = pl.pf_items_max;
-    p.pf_seq = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_items) : nullptr;
+    p.pf_count = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_items) : nullptr;
+    p.pf_seq = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_items + 256) : nullptr;
     p.pf_rt = pl.pf_items_max ? p.pf_seq + pl.pf_items_max : nullptr;
+    // decode workspace pointers are set per decode class in launch_all
+    p.ws_hdr = nullptr;
+    p.ws_pre = nullptr;
+    p.ws_ml = nullptr;
+    p.ws_o = nullptr;
+    p.nwg = 0;
 
 #define GFA_DISPATCH_O(QDT)                                                                    \
     switch (out_dtype) {                                                                       \
-        case GFA_DTYPE_F32: return launch_all<QDT, GFA_DTYPE_F32>(p, pl, num_seqs, num_kv_heads, max_query_len, stream); \
-        case GFA_DTYPE_F16: return launch_all<QDT, GFA_DTYPE_F16>(p, pl, num_seqs, num_kv_heads, max_query_len, stream); \
-        default: return launch_all<QDT, GFA_DTYPE_BF16>(p, pl, num_seqs, num_kv_heads, max_query_len, stream); \
+        case GFA_DTYPE_F32: return launch_all<QDT, GFA_DTYPE_F32>(p, pl, ws, num_seqs, num_kv_heads, max_query_len, stream); \
+        case GFA_DTYPE_F16: return launch_all<QDT, GFA_DTYPE_F16>(p, pl, ws, num_seqs, num_kv_heads, max_query_len, stream); \
+        default: return launch_all<QDT, GFA_DTYPE_BF16>(p, pl, ws, num_seqs, num_kv_heads, max_query_len, stream); \
     }
     switch (q_dtype) {
         case GFA_DTYPE_F32: GFA_DISPATCH_O(GFA_DTYPE_F32);

@@ -65,11 +65,16 @@ class Gfx906FAMetadata:
     common_prefix_len: int = 0
 
 
-def workspace_upper_bound(max_num_seqs: int) -> int:
+def workspace_upper_bound(max_num_seqs: int, max_query_len: int = 16) -> int:
     """Attention workspace that covers every batch of up to max_num_seqs
-    sequences (32-row decode tiles, the larger slot size; the workspace does
-    not depend on context lengths)."""
-    return gfx906_fa.workspace_size(max_num_seqs, max_num_seqs, 32, 1, 1, 1)
+    sequences of up to max_query_len tokens (the workspace does not depend on
+    context lengths): the largest of a uniform 32-row decode batch, a mixed
+    batch using both decode classes and a prefill work list, and a uniform
+    batch that goes to the prefill kernel."""
+    B, q = max_num_seqs, max(int(max_query_len), 2)
+    return max(gfx906_fa.workspace_size(B, B, 32, 1, 1, 1),
+               gfx906_fa.workspace_size(B, B * q - 1, 16, 1, q, 1),
+               gfx906_fa.workspace_size(B, B * q, 128, 1, q, 1))
 
 
 class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
