@@ -584,12 +584,16 @@ template <int NRG, int ODT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     constexpr int R = 16 * NRG;
     const int s = blockIdx.x, h = blockIdx.y, r = blockIdx.z;
-    const SegInfo si = seg_info(p, s);
-    if (si.nsub == 0 || r >= si.nq * p.G) return;
+    // the plan words are read together with the sequence's metadata (one
+    // memory round trip instead of two: they are needed only when the
+    // segment turns out to be split)
     const int64_t U = p.ws_hdr[0];
     const int nwg = (int)p.ws_hdr[1];
+    const int pre = p.ws_pre[s];
+    const SegInfo si = seg_info(p, s);
+    if (si.nsub == 0 || r >= si.nq * p.G) return;
     if (U == 0) return;
-    const int64_t S0 = (int64_t)p.ws_pre[s] * p.Hkv + (int64_t)h * si.nsub;
+    const int64_t S0 = (int64_t)pre * p.Hkv + (int64_t)h * si.nsub;
     const int wf = range_of(U, S0, nwg), wl = range_of(U, S0 + si.nsub - 1, nwg);
     if (wf == wl && range_start(U, wf, nwg) <= S0 && range_start(U, wf + 1, nwg) >= S0 + si.nsub)
         return;  // whole segment in one workgroup: already written

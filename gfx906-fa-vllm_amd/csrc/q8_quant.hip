@@ -101,13 +101,8 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
     if (wave >= num_tokens * num_kv_heads) return;
     const int t = wave / num_kv_heads;
     const int h = wave - t * num_kv_heads;
-    const int64_t slot = slot_mapping[t];
-    if (slot < 0) return;
-    const int64_t page = slot / block_size;
-    const int off = (int)(slot - page * block_size);
-    const int sp = off >> 4, tt = off & 15;
-    const int64_t base = page * cbs + (int64_t)h * chs + (int64_t)sp * SUBPAGE_BYTES;
-
+    // the row's values are loaded before the slot test (they are valid input
+    // rows either way), so the slot and value loads share one memory round trip
     const int d0 = 2 * lane;
     float ka, kb, va, vb;
     if constexpr (VEC) {
@@ -119,6 +114,12 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
         va = load_as_f32<DT>(value, (int64_t)t * vts + (int64_t)h * vhs + d0);
         vb = load_as_f32<DT>(value, (int64_t)t * vts + (int64_t)h * vhs + d0 + 1);
     }
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) return;
+    const int64_t page = slot / block_size;
+    const int off = (int)(slot - page * block_size);
+    const int sp = off >> 4, tt = off & 15;
+    const int64_t base = page * cbs + (int64_t)h * chs + (int64_t)sp * SUBPAGE_BYTES;
     const Q8Pair rk = q8_quantize_pair(ka, kb);
     const Q8Pair rv = q8_quantize_pair(va, vb);
 
@@ -249,6 +250,10 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_blk_kernel(
         f32_to_half_bits(d);
 }
 
+#ifndef GFA_WRITE_ROW_KERNEL_MAX
+#define GFA_WRITE_ROW_KERNEL_MAX 4096  // (token, kv-head) rows
+#endif
+
 bool bad_dtype(int dt) { return dt != GFA_DTYPE_F32 && dt != GFA_DTYPE_F16 && dt != GFA_DTYPE_BF16; }
 
 }  // namespace
@@ -336,7 +341,12 @@ extern "C" hipError_t gfx906_fa_amd_cache_write_kv(
     const int esz = dtype == GFA_DTYPE_F32 ? 4 : 2;
     const bool vec = (((uintptr_t)key | (uintptr_t)value) % (2 * esz) == 0) && (kts % 2 == 0) &&
                      (khs % 2 == 0) && (vts % 2 == 0) && (vhs % 2 == 0);
-    if ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uint64_t)cbs | (uint64_t)chs) & 7u) == 0) {
+    // Small batches (decode steps) take the wave-per-row kernel: its serial
+    // work per lane is one pair of values, so a handful of rows finishes in
+    // the latency of its loads; the block-per-lane kernel's 32-value serial
+    // quantize only pays once there are enough rows to fill the device.
+    const bool few_rows = (int64_t)num_tokens * num_kv_heads <= GFA_WRITE_ROW_KERNEL_MAX;
+    if (!few_rows && (((uintptr_t)k_cache | (uintptr_t)v_cache | (uint64_t)cbs | (uint64_t)chs) & 7u) == 0) {
         // block per lane: vector loads need 16-byte aligned rows of 32 values
         const bool vec16 = (((uintptr_t)key | (uintptr_t)value) % 16 == 0) &&
                            ((kts * esz) % 16 == 0) && ((khs * esz) % 16 == 0) &&

@@ -48,6 +48,10 @@ from gfx906_fa_paged import forward_paged, q8_planes
 
 logger = init_logger(__name__)
 
+# kv_cache_dtype of the cache whose pages hold exactly the Q8_0 planes
+Q8_CACHE_DTYPE = "q8_0"
+_KV_CACHE_DTYPES = ("auto", "float16", "half", "bfloat16", Q8_CACHE_DTYPE)
+
 
 # -----------------------------------------------------------------------------
 # Metadata (reference lines 59-109)
@@ -121,9 +125,13 @@ class Gfx906FABackend(AttentionBackend):
     accept_output_buffer: bool = True
 
     supported_dtypes: ClassVar[list[torch.dtype]] = [torch.float16, torch.bfloat16]
-    # vLLM allocates the pages in the model dtype; the Q8_0 planes are stored
-    # inside them (gfx906_fa_paged.q8_planes).
-    supported_kv_cache_dtypes: ClassVar[list[CacheDType]] = ["auto", "float16", "half", "bfloat16"]
+    # "auto" / "float16" / "half" / "bfloat16": vLLM allocates the pages in the
+    # model dtype and the Q8_0 planes are stored inside them (the first 272 of
+    # every 512 bytes per token and kv-head are used).  "q8_0": pages of
+    # exactly the Q8_0 planes, 272 bytes per token and kv-head (1.88x the
+    # tokens per GiB); needs vLLM to size the page with q8_page_size_bytes().
+    supported_kv_cache_dtypes: ClassVar[list[CacheDType]] = ["auto", "float16", "half", "bfloat16",
+                                                             Q8_CACHE_DTYPE]
 
     forward_includes_kv_cache_update: bool = False
 
@@ -150,8 +158,36 @@ class Gfx906FABackend(AttentionBackend):
                            cache_dtype_str: str = "auto") -> tuple[int, ...]:
         if block_size % 16 != 0:
             raise ValueError("Block size must be a multiple of 16.")
+        if cache_dtype_str == Q8_CACHE_DTYPE:
+            # uint8 page = [K plane | V plane], each [Hkv][block_size/16
+            # sub-pages][2176 B]; five dims so vLLM's identity stride order
+            # applies unchanged
+            if head_size != 128:
+                raise ValueError("the Q8_0 page layout needs head_size 128")
+            return (num_blocks, 2, num_kv_heads, block_size // 16, gfx906_fa.SUBPAGE_BYTES)
         # Same as TritonAttentionBackend, so the allocator is unchanged.
         return (num_blocks, 2, block_size, num_kv_heads, head_size)
+
+    @staticmethod
+    def q8_page_size_bytes(block_size: int, num_kv_heads: int, head_size: int = 128) -> int:
+        """Bytes of one page of the "q8_0" cache: K and V Q8_0 rows of
+        block_size tokens x num_kv_heads, (head_size/32)*34 bytes each
+        (extension/gfx906_fa_quant.cu:142-145 sizes the reference's K rows
+        the same way).  vLLM's page for this cache dtype must be exactly this
+        (a uint8 FullAttentionSpec padded to it)."""
+        if block_size % 16 != 0 or head_size != 128:
+            raise ValueError("the Q8_0 page layout needs block_size % 16 == 0 and head_size 128")
+        return 2 * num_kv_heads * (block_size // 16) * gfx906_fa.SUBPAGE_BYTES
+
+    @staticmethod
+    def get_kv_cache_page_size_bytes(block_size: int, num_kv_heads: int, head_size: int,
+                                     cache_dtype_str: str, model_dtype: torch.dtype) -> int:
+        """Page bytes for either cache layout (what vLLM's KV-cache spec has
+        to allocate per block)."""
+        if cache_dtype_str == Q8_CACHE_DTYPE:
+            return Gfx906FABackend.q8_page_size_bytes(block_size, num_kv_heads, head_size)
+        itemsize = torch.empty((), dtype=model_dtype).element_size()
+        return 2 * block_size * num_kv_heads * head_size * itemsize
 
     @staticmethod
     def get_kv_cache_stride_order(include_num_layers_dimension: bool = False) -> tuple[int, ...]:
@@ -221,6 +257,8 @@ class Gfx906FAImpl(AttentionImpl):
             raise NotImplementedError(f"GFX906_FA: head_size={head_size} is not supported (128 only)")
         if num_heads % num_kv_heads != 0:
             raise ValueError("num_heads must be a multiple of num_kv_heads")
+        if kv_cache_dtype not in _KV_CACHE_DTYPES:
+            raise NotImplementedError(f"GFX906_FA: kv_cache_dtype={kv_cache_dtype} is not supported")
         self.num_heads = num_heads
         self.head_size = head_size
         self.scale = float(scale)

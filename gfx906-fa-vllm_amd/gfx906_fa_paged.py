@@ -38,12 +38,24 @@ def q8_planes(kv_cache: torch.Tensor, num_kv_heads: int, head_size: int,
     Accepted layouts:
       * the planar cache itself, uint8 [NB, 2, Hkv, block_size/16*2176]
         (``gfx906_fa.new_kv_cache``);
+      * the backend's "q8_0" page, uint8 [NB, 2, Hkv, block_size/16, 2176]
+        (``Gfx906FABackend.get_kv_cache_shape(..., "q8_0")``): the same bytes
+        as the planar cache, viewed with the sub-page as its own dimension;
       * vLLM's per-layer tensor [NB, 2, bs, Hkv, D] in fp16/bf16/fp32
         (``Gfx906FABackend.get_kv_cache_shape``, identical to the reference's
         ``extension/gfx906_fa_backend.py:153-165``).  Each page's bytes hold
         the K plane then the V plane of that page; 136/256 of an fp16 page is
-        used (a dedicated Q8 page size is vLLM-side integration work).
+        used (the "q8_0" page above holds the same bytes with no slack).
     """
+    if kv_cache.dtype == torch.uint8 and kv_cache.dim() == 5:
+        NB, two, Hkv, nsp, sub = kv_cache.shape
+        if two != 2 or Hkv != num_kv_heads or sub != SUBPAGE_BYTES or head_size != 128:
+            raise RuntimeError("q8_0 pages must be uint8 [NB, 2, Hkv, bs/16, 2176] (head_size 128)")
+        if block_size is not None and nsp * SUBPAGE_TOKENS != block_size:
+            raise RuntimeError(f"block_size mismatch {nsp * SUBPAGE_TOKENS} vs {block_size}")
+        if kv_cache.stride(4) != 1 or kv_cache.stride(3) != SUBPAGE_BYTES:
+            raise RuntimeError("q8_0 pages must be contiguous within a kv-head")
+        kv_cache = kv_cache.flatten(3)
     if kv_cache.dtype == torch.uint8 and kv_cache.dim() == 4:
         if kv_cache.shape[1] != 2 or kv_cache.shape[2] != num_kv_heads:
             raise RuntimeError("planar cache must be [NB, 2, Hkv, bs/16*2176]")

@@ -86,6 +86,54 @@ def test_q8_planes_inside_vllm_pages():
     assert k2.data_ptr() == planar.data_ptr()
 
 
+def _vllm_style_cache(backend, NB, bs, Hkv, D, cache_dtype, model_dtype):
+    """What vLLM's allocator does with a backend: one raw int8 buffer of
+    page_size x num_blocks bytes, viewed in the cache dtype and the backend's
+    shape."""
+    page = backend.get_kv_cache_page_size_bytes(bs, Hkv, D, cache_dtype, model_dtype)
+    raw = torch.zeros(page * NB, dtype=torch.int8)
+    dt = torch.uint8 if cache_dtype == "q8_0" else model_dtype
+    return raw.view(dt).view(backend.get_kv_cache_shape(NB, bs, Hkv, D, cache_dtype)), page
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64])
+def test_q8_0_pages_hold_exactly_the_planes(bs):
+    """The "q8_0" cache dtype: pages of 272 B per token and kv-head, whose
+    planes sit at the same offsets inside the page as in an fp16 page (so the
+    kernels see the same bytes; only the page stride shrinks)."""
+    from gfx906_fa_backend import Gfx906FABackend, Gfx906FAImpl
+    from gfx906_fa_paged import q8_planes
+    NB, Hkv, D = 6, 8, 128
+    assert "q8_0" in Gfx906FABackend.supported_kv_cache_dtypes
+    q8, page_q8 = _vllm_style_cache(Gfx906FABackend, NB, bs, Hkv, D, "q8_0", torch.float16)
+    f16, page_f16 = _vllm_style_cache(Gfx906FABackend, NB, bs, Hkv, D, "auto", torch.float16)
+    assert page_q8 == bs * Hkv * 2 * (D // 32 * 34)          # 272 B per token and kv-head
+    assert page_f16 == bs * Hkv * 2 * D * 2 and page_f16 * 136 == page_q8 * 256
+    assert q8.shape == (NB, 2, Hkv, bs // 16, 2176)
+    kq, vq = q8_planes(q8, Hkv, D, block_size=bs)
+    kf, vf = q8_planes(f16, Hkv, D, block_size=bs)
+    assert kq.shape == kf.shape == vq.shape == vf.shape == (NB, Hkv, bs // 16 * 2176)
+    assert kq.stride() == (page_q8, bs // 16 * 2176, 1) and vq.stride() == kq.stride()
+    for (k, v, base, page) in ((kq, vq, q8.data_ptr(), page_q8), (kf, vf, f16.data_ptr(), page_f16)):
+        assert k.data_ptr() - base == 0
+        assert v.data_ptr() - base == Hkv * bs // 16 * 2176     # V plane after every K plane
+    # every byte of a q8_0 page belongs to exactly one plane
+    marks = torch.zeros(page_q8 * NB, dtype=torch.uint8)
+    mv = marks.view(q8.shape)
+    km, vm = q8_planes(mv, Hkv, D)
+    km.add_(1)
+    vm.add_(2)
+    assert set(marks.unique().tolist()) == {1, 2}
+    assert int((marks == 1).sum()) == int((marks == 2).sum()) == NB * bs * Hkv * 136
+    Gfx906FAImpl(8, 128, 0.1, 1, None, None, "q8_0")          # accepted
+    with pytest.raises(NotImplementedError):
+        Gfx906FAImpl(8, 128, 0.1, 1, None, None, "fp8")
+    with pytest.raises(ValueError):
+        Gfx906FABackend.get_kv_cache_shape(NB, bs, Hkv, 64, "q8_0")
+    with pytest.raises(RuntimeError):
+        q8_planes(q8, Hkv, D, block_size=2 * bs)
+
+
 def test_graph_support_and_workspace_bound():
     """The builder declares graph support for uniform batches; the workspace
     it reserves up front covers every batch of up to max_num_seqs sequences,

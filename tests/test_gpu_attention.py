@@ -210,6 +210,70 @@ def test_backend_impl_end_to_end():
     assert_close(output.float().cpu().numpy().reshape(Hq, D), ref, extra=2.0 ** -11)
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_backend_q8_0_pages_match_fp16_pages(bs):
+    """The "q8_0" cache dtype (pages of exactly the Q8_0 planes) against the
+    default fp16-sized pages: the same writes give the same plane bytes, and
+    a mixed prefill + decode forward gives bit-identical outputs, in
+    tolerance of the oracle."""
+    need_gpu()
+    announce(f"backend q8_0 pages vs fp16 pages bs={bs}")
+    from gfx906_fa_backend import Gfx906FABackend, Gfx906FAImpl, Gfx906FAMetadata
+    from gfx906_fa_paged import q8_planes
+    Hq, Hkv, D, NB = 16, 4, 128, 40
+    rng = np.random.default_rng(21)
+    torch.manual_seed(21)
+    sl = [300, 41, 170]
+    ql = [300, 1, 5]
+    nblk = [(n + bs - 1) // bs for n in sl]
+    perm = rng.permutation(NB)[:sum(nblk)]
+    bt = np.full((3, max(nblk)), -1, np.int32)
+    o = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[o:o + n]
+        o += n
+    btt = torch.from_numpy(bt).to(DEV)
+    caches = {}
+    for cd in ("auto", "q8_0"):
+        page = Gfx906FABackend.get_kv_cache_page_size_bytes(bs, Hkv, D, cd, torch.float16)
+        raw = torch.zeros(page * NB, dtype=torch.int8, device=DEV)
+        caches[cd] = raw.view(torch.uint8 if cd == "q8_0" else torch.float16).view(
+            Gfx906FABackend.get_kv_cache_shape(NB, bs, Hkv, D, cd))
+    keys = [torch.randn((n, Hkv, D), dtype=torch.float16, device=DEV) for n in sl]
+    vals = [torch.randn((n, Hkv, D), dtype=torch.float16, device=DEV) for n in sl]
+    slots = []
+    for s, n in enumerate(sl):
+        pos = torch.arange(n, device=DEV)
+        slots.append(btt[s, pos // bs].long() * bs + pos % bs)
+    q = torch.randn((sum(ql), Hq, D), dtype=torch.float16, device=DEV)
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(ql)]), dtype=torch.int32, device=DEV)
+    outs = {}
+    for cd, kv in caches.items():
+        impl = Gfx906FAImpl(Hq, D, 1 / math.sqrt(D), Hkv, None, None, cd)
+        for s, n in enumerate(sl):       # context first, then the step's new tokens
+            k = ql[s]
+            impl.do_kv_cache_update(None, keys[s][:n - k], vals[s][:n - k], kv, slots[s][:n - k])
+        nk = torch.cat([keys[s][n - ql[s]:] for s, n in enumerate(sl)])
+        nv = torch.cat([vals[s][n - ql[s]:] for s, n in enumerate(sl)])
+        ns = torch.cat([slots[s][n - ql[s]:] for s, n in enumerate(sl)])
+        impl.do_kv_cache_update(None, nk, nv, kv, ns)
+        md = Gfx906FAMetadata(num_actual_tokens=sum(ql), max_query_len=max(ql), max_seq_len=max(sl),
+                              query_start_loc=qsl, seq_lens=torch.tensor(sl, dtype=torch.int32, device=DEV),
+                              block_table=btt, slot_mapping=ns)
+        out = torch.empty((sum(ql), Hq * D), dtype=torch.float16, device=DEV)
+        impl.forward(None, q, nk, nv, kv, md, output=out)
+        outs[cd] = out
+    torch.cuda.synchronize()
+    (kf, vf), (kq, vq) = q8_planes(caches["auto"], Hkv, D), q8_planes(caches["q8_0"], Hkv, D)
+    assert torch.equal(kf, kq) and torch.equal(vf, vq)
+    assert torch.equal(outs["auto"], outs["q8_0"])
+    planar = torch.stack([kq, vq], 1).cpu().numpy()
+    kh, vh = O.planar_dequant(planar)
+    ref = O.paged_attention_ref(q.float().cpu().numpy(), kh, vh, bt, np.asarray(sl, np.int32),
+                                qsl.cpu().numpy(), 1 / math.sqrt(D))
+    assert_close(outs["q8_0"].float().cpu().numpy().reshape(-1, Hq, D), ref, extra=2.0 ** -11)
+
+
 # ---------------------------------------------------------------------------
 # Full-size configurations: sampled-row parity + permutation invariance
 # ---------------------------------------------------------------------------

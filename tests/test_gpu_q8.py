@@ -133,6 +133,28 @@ def test_cache_write_kv_planar(dt, bs):
     assert np.array_equal(cache.cpu().numpy(), exp)
 
 
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_cache_write_kv_planar_many_rows(dt, bs):
+    """Above 4096 (token, kv-head) rows the write takes the block-per-lane
+    kernel (one Q8_0 block per lane, 16 tokens per wave); a ragged last group
+    of tokens and skipped slots included.  Bit-exact like the small path."""
+    need_gpu()
+    announce(f"cache_write_kv planar many rows {dt} bs={bs}")
+    rng = np.random.default_rng(15)
+    Hkv, T = 4, 1100            # 4400 rows; T % 16 = 12
+    NB = (T + 40) // bs + 1
+    key = _rand((T, Hkv, 128), dt, 1.0, seed=16)
+    val = _rand((T, Hkv, 128), dt, 2.0, seed=17)
+    slots = rng.permutation(NB * bs)[:T].astype(np.int64)
+    slots[[0, 17, 1099]] = -1
+    cache = torch.full((NB, 2, Hkv, bs // 16 * 2176), 0x3C, dtype=torch.uint8, device=DEV)
+    gfx906_fa.reshape_and_cache_q8_kv(key, val, torch.from_numpy(slots).to(DEV), cache[:, 0], cache[:, 1])
+    exp = np.full(tuple(cache.shape), 0x3C, np.uint8)
+    O.planar_cache_write(host_bits(key), host_bits(val), slots, exp)
+    assert np.array_equal(cache.cpu().numpy(), exp)
+
+
 def test_cache_write_kv_strided_inputs():
     need_gpu()
     announce("cache_write_kv strided inputs")
