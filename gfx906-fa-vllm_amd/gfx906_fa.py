@@ -21,6 +21,8 @@ forward_paged_direct(q, key_cache_q8, value_cache, block_table, seq_lens,
                                                        extension/gfx906_fa.cpp:516-658
 New for the Q8 K+V cache of this backend:
 reshape_and_cache_q8_kv(key, value, slot_mapping, key_cache, value_cache)
+rope_and_cache_q8_kv(positions, query, key, value, cos_sin_cache, is_neox,
+                     slot_mapping, key_cache, value_cache, rot_dim=None)
 gather_paged_kv_q8q8(key_cache, value_cache, block_table, seq_lens, Sk, ...)
 paged_attention(query, key_cache, value_cache, block_table, seq_lens,
                 query_start_loc, max_query_len, max_seq_len, scale, out=None, ...)
@@ -70,6 +72,8 @@ def _load():
         "gfx906_fa_amd_gather_planar": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I64, I64, P]),
         "gfx906_fa_amd_cache_write_kv": (I, [P, P, I, P, P, P, I, I, I, I,
                                              I64, I64, I64, I64, I64, I64, P]),
+        "gfx906_fa_amd_rope_cache_write_kv": (I, [P, P, P, I, P, P, I, I64, I, I, I, P, P, P, I, I, I, I, I,
+                                                  I64, I64, I64, I64, I64, I64, I64, I64, P]),
         "gfx906_fa_amd_paged_attention_workspace_size": (SZ, [I, I, I, I, I, I, I]),
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
@@ -274,6 +278,50 @@ def reshape_and_cache_q8_kv(key: torch.Tensor, value: torch.Tensor, slot_mapping
         Hkv, D, bs, key.stride(0), key.stride(1), value.stride(0), value.stride(1), cbs, chs,
         _stream(key.device))
     _ok(err, "gfx906_fa_amd_cache_write_kv")
+
+
+def rope_and_cache_q8_kv(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor,
+                         value: torch.Tensor, cos_sin_cache: torch.Tensor, is_neox: bool,
+                         slot_mapping: torch.Tensor, key_cache: torch.Tensor,
+                         value_cache: torch.Tensor, rot_dim: Optional[int] = None) -> None:
+    """Rotary embedding of query [T, Hq, 128] and key [T, Hkv, 128] in place
+    (vLLM semantics: cos/sin rows of cos_sin_cache [max_position, rot_dim]
+    at ``positions`` (int64), converted to the model dtype; neox or GPT-J
+    pairs; per-operation rounding in the model dtype), then the rotated key
+    and the value quantized to Q8_0 at slot_mapping (< 0 skips) - one launch.
+    Positions outside [0, max_position) leave their rows unrotated."""
+    for t, n in ((positions, "positions"), (query, "query"), (key, "key"), (value, "value"),
+                 (cos_sin_cache, "cos_sin_cache"), (slot_mapping, "slot_mapping"),
+                 (key_cache, "key_cache"), (value_cache, "value_cache")):
+        _cuda(t, n)
+    _check(query.dtype in (torch.float16, torch.bfloat16) and key.dtype == query.dtype
+           and value.dtype == query.dtype, "query/key/value must share dtype fp16 or bf16")
+    _check(query.dim() == 3 and key.dim() == 3 and value.shape == key.shape and query.shape[0] == key.shape[0],
+           "query must be [T, Hq, D], key/value [T, Hkv, D]")
+    _check(positions.dtype == torch.int64 and positions.dim() == 1 and positions.shape[0] == query.shape[0],
+           "positions must be int64 [num_tokens]")
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.shape[0] == query.shape[0],
+           "slot_mapping must be int64 [num_tokens]")
+    _check(cos_sin_cache.dtype in _DT and cos_sin_cache.dim() == 2 and cos_sin_cache.stride(1) == 1,
+           "cos_sin_cache must be [max_position, rot_dim] with contiguous rows")
+    T, Hq, D = query.shape
+    Hkv = key.shape[1]
+    _check(D == 128 and key.shape[2] == 128, "head_size must be 128")
+    for t, n in ((query, "query"), (key, "key"), (value, "value")):
+        _check(t.stride(2) == 1, f"{n} rows must be contiguous")
+    rot = cos_sin_cache.shape[1] if rot_dim is None else int(rot_dim)
+    bs, Hc, cbs, chs = _plane_info(key_cache, value_cache)
+    _check(Hc == Hkv, f"cache Hkv mismatch: got {Hc} vs key Hkv={Hkv}")
+    _check(Hq % Hkv == 0, f"heads_q={Hq} must be divisible by heads_kv={Hkv}")
+    pos = positions.contiguous()
+    sm = slot_mapping.contiguous()
+    err = _load().gfx906_fa_amd_rope_cache_write_kv(
+        _ptr(query), _ptr(key), _ptr(value), _DT[query.dtype], _ptr(pos), _ptr(cos_sin_cache),
+        _DT[cos_sin_cache.dtype], cos_sin_cache.stride(0), cos_sin_cache.shape[0], rot, 1 if is_neox else 0,
+        _ptr(sm), _ptr(key_cache), _ptr(value_cache), T, Hq, Hkv, D, bs,
+        query.stride(0), query.stride(1), key.stride(0), key.stride(1), value.stride(0), value.stride(1),
+        cbs, chs, _stream(query.device))
+    _ok(err, "gfx906_fa_amd_rope_cache_write_kv")
 
 
 def gather_paged_kv_q8q8(key_cache: torch.Tensor, value_cache: torch.Tensor,

@@ -272,7 +272,27 @@ class Gfx906FAImpl(AttentionImpl):
         return False
 
     def fused_rope_kvcache_supported(self):
-        return False
+        # do_rope_and_kv_cache_update rotates query/key and writes the Q8_0
+        # cache in one launch (the reference returns False,
+        # extension/gfx906_fa_backend.py:444-445)
+        return True
+
+    def do_rope_and_kv_cache_update(self, layer: AttentionLayer, query: torch.Tensor,
+                                    key: torch.Tensor, value: torch.Tensor, positions: torch.Tensor,
+                                    cos_sin_cache: torch.Tensor, is_neox: bool, kv_cache: torch.Tensor,
+                                    layer_slot_mapping: torch.Tensor):
+        """vLLM's fused rope + KV-cache update: query [T, Hq*D] / [T, Hq, D]
+        and key are rotated in place (vLLM rotary semantics), and the rotated
+        key and the value go into the Q8_0 cache at layer_slot_mapping."""
+        kp, vp = q8_planes(kv_cache, self.num_kv_heads, self.head_size)
+        n = layer_slot_mapping.shape[0]
+        D = self.head_size
+        q = query[:n].view(n, self.num_heads, D)
+        k = key[:n].view(n, self.num_kv_heads, D)
+        v = value[:n].view(n, self.num_kv_heads, D)
+        pos = positions[:n] if positions.dtype == torch.int64 else positions[:n].to(torch.int64)
+        sm = layer_slot_mapping if layer_slot_mapping.dtype == torch.int64 else layer_slot_mapping.to(torch.int64)
+        gfx906_fa.rope_and_cache_q8_kv(pos, q, k, v, cos_sin_cache, is_neox, sm, kp, vp)
 
     @classmethod
     def reserve_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor:

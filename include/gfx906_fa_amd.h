@@ -144,6 +144,33 @@ hipError_t gfx906_fa_amd_cache_write_kv(
     int64_t value_token_stride, int64_t value_head_stride, int64_t cache_block_stride,
     int64_t cache_head_stride, hipStream_t stream);
 
+/* (4b) Fused rotary embedding + (4).  query [T, Hq, D] and key [T, Hkv, D]
+ *      are rotated in place, then the rotated key and value are written as
+ *      (4) does.  Rotary semantics (vLLM's rotary embedding): cos and sin are
+ *      cos_sin_cache[positions[t]][0 .. rot_dim/2) and [rot_dim/2 .. rot_dim)
+ *      (row stride cos_sin_stride elements, dtype cos_sin_dtype), converted
+ *      to the model dtype; each pair (x, y) - (i, i + rot_dim/2) when
+ *      is_neox, else (2i, 2i+1) - becomes (x*cos - y*sin, y*cos + x*sin)
+ *      with every operation rounded to the model dtype; dims >= rot_dim are
+ *      untouched.  Positions outside [0, max_position) leave their rows
+ *      unrotated (nothing is read out of the cos/sin table).
+ *      Requirements: fp16/bf16, D = 128, rot_dim <= 128 and a multiple of 16
+ *      (neox) or 8, q/k/v rows 16-byte aligned (element strides multiples of
+ *      8), cos/sin rows 8-byte aligned.
+ *      Replaces the reference backend's declared absence of this fusion
+ *      (fused_rope_kvcache_supported() returning False,
+ *      extension/gfx906_fa_backend.py:444-445) for vLLM's fused
+ *      rope + KV-cache-update path.
+ */
+hipError_t gfx906_fa_amd_rope_cache_write_kv(
+    void *query, void *key, const void *value, int dtype, const int64_t *positions,
+    const void *cos_sin_cache, int cos_sin_dtype, int64_t cos_sin_stride, int max_position,
+    int rot_dim, int is_neox, const int64_t *slot_mapping, uint8_t *k_cache, uint8_t *v_cache,
+    int num_tokens, int num_heads, int num_kv_heads, int head_size, int block_size,
+    int64_t query_token_stride, int64_t query_head_stride, int64_t key_token_stride,
+    int64_t key_head_stride, int64_t value_token_stride, int64_t value_head_stride,
+    int64_t cache_block_stride, int64_t cache_head_stride, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * (5) Varlen direct-paged attention over the planar Q8 K+V cache: decode,
  *     chunked prefill, mixed batches and speculative verify in one call.

@@ -42,6 +42,12 @@ Pinning (what checks each function beyond restating it):
 * ``planar_*`` - the MI355X page layouts of this build (not reference
   formats); pinned by round trips against the AoS / fp16 rows (each
   position map a bijection onto its sub-page).
+* ``rope_ref`` - vLLM's rotary embedding (third-party, absent here; the
+  reference's hook is ``extension/gfx906_fa_backend.py:444-445``).  Pinned
+  by: an independent torch CPU restatement of vLLM's native form (16-bit
+  tensor ops) agreeing bit for bit; the complex product
+  (x1 + i x2)(cos + i sin) in float64 agreeing to the dtype's rounding (fixes
+  the pairing and the signs); identity at angle 0; pairwise norms kept.
 """
 from __future__ import annotations
 
@@ -481,3 +487,68 @@ def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
 
 def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Rotary embedding (the fused rope + cache write)
+# ---------------------------------------------------------------------------
+# The reference declares no fused rope + KV write (its backend returns False
+# from fused_rope_kvcache_supported, extension/gfx906_fa_backend.py:444-445);
+# the rotary arithmetic belongs to vLLM (0.19.1, pinned by the reference's
+# README.md:29 and docker/Dockerfile:24; not vendored, not installed here).
+# Its published form (RotaryEmbedding.forward_native / _apply_rotary_emb_torch,
+# and the device kernel apply_token_rotary_embedding) is restated below:
+#   cos, sin = cos_sin_cache[pos].chunk(2); cos, sin -> x.dtype
+#   neox:  x1, x2 = x[..., :rot/2], x[..., rot/2:rot]
+#   gptj:  x1, x2 = x[..., 0:rot:2], x[..., 1:rot:2]
+#   o1 = x1*cos - x2*sin;  o2 = x2*cos + x1*sin     (each op in x.dtype)
+# A 16-bit tensor op is computed in float32 and rounded once to the tensor's
+# dtype, so every product, difference and sum is rounded here too.
+def _round_model(x32: np.ndarray, bf16: bool) -> np.ndarray:
+    """float32 -> model dtype (fp16 or bf16, RNE) -> float32."""
+    x32 = np.asarray(x32, dtype=np.float32)
+    if bf16:
+        return bf16_bits_to_f32(f32_to_bf16_bits(x32))
+    return x32.astype(np.float16).astype(np.float32)
+
+
+def rope_cos_sin_cache(max_position: int, rot_dim: int, base: float = 10000.0) -> np.ndarray:
+    """float32 [max_position, rot_dim]: cos | sin of position * base^(-2i/rot)
+    (vLLM's RotaryEmbedding._compute_cos_sin_cache)."""
+    inv = 1.0 / (base ** (np.arange(0, rot_dim, 2, dtype=np.float32) / rot_dim))
+    f = np.outer(np.arange(max_position, dtype=np.float32), inv.astype(np.float32)).astype(np.float32)
+    return np.concatenate([np.cos(f), np.sin(f)], axis=-1).astype(np.float32)
+
+
+def rope_ref(x, positions: np.ndarray, cos_sin, rot_dim: int, is_neox: bool):
+    """Rotary embedding of x [T, H, D] (fp16, or bf16 as uint16 bits) at
+    positions [T]; returns the same dtype.  cos_sin [P, >= rot_dim] in
+    float32, fp16 or bf16 bits (converted to x's dtype first).  Rows whose
+    position is outside [0, P) are returned unchanged."""
+    x = np.asarray(x)
+    bf16 = x.dtype == np.uint16
+    xf = _to_f32(x).copy()                           # [T, H, D]
+    cs = _to_f32(np.asarray(cos_sin))
+    P = cs.shape[0]
+    half = rot_dim // 2
+    pos = np.asarray(positions, dtype=np.int64)
+    ok = (pos >= 0) & (pos < P)
+    p = np.where(ok, pos, 0)
+    c = _round_model(cs[p, :half], bf16)[:, None, :]          # [T, 1, half]
+    s = _round_model(cs[p, half:rot_dim], bf16)[:, None, :]
+    r = lambda a: _round_model(a, bf16)                         # noqa: E731
+    if is_neox:
+        x1, x2 = xf[..., :half], xf[..., half:rot_dim]
+    else:
+        x1, x2 = xf[..., 0:rot_dim:2], xf[..., 1:rot_dim:2]
+    o1 = r(r(x1 * c) - r(x2 * s))
+    o2 = r(r(x2 * c) + r(x1 * s))
+    out = xf.copy()
+    if is_neox:
+        out[..., :half], out[..., half:rot_dim] = o1, o2
+    else:
+        out[..., 0:rot_dim:2], out[..., 1:rot_dim:2] = o1, o2
+    out[~ok] = xf[~ok]
+    if bf16:
+        return f32_to_bf16_bits(out)
+    return out.astype(np.float16)
