@@ -79,6 +79,12 @@ struct AttnParams {
     // nullptr: the prefill grid is (row tiles * Hkv, num_seqs) instead.
     int *pf_seq, *pf_rt, *pf_count;
     int pf_items_max;
+    // Fused cache write of the step's new tokens (decode kernels only; nullptr:
+    // none).  Row qsl[s] + j of new_k / new_v (the query dtype) holds the key /
+    // value of position seq_lens[s] - n_q + j, written at slot new_slot[row].
+    const void *new_k, *new_v;
+    int64_t nk_ts, nk_hs, nv_ts, nv_hs;  // element strides
+    const int64_t *new_slot;
 };
 
 __device__ __forceinline__ float4_t mfma16(half8_t a, half8_t b, float4_t c) {
@@ -373,6 +379,28 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
 //
 // Register budget: one row group runs GFA_DEC_WPE waves per SIMD; two row
 // groups (speculative verify) need twice the accumulators and run 2.
+// One new (token, kv-head) row of the fused cache write: input row `row` of
+// new_k / new_v quantized to Q8_0 (two values per lane, a block per 16-lane
+// DPP row, the closed form of the cache-write kernel) and stored at
+// new_slot[row] (< 0: nothing).  The whole wave takes part.
+template <int DT>
+__device__ __forceinline__ void write_new_token(const AttnParams &p, int h, int64_t row, int lane) {
+    const int d0 = 2 * lane;
+    float ka, kb, va, vb;
+    load2_as_f32<DT>(p.new_k, row * p.nk_ts + (int64_t)h * p.nk_hs + d0, ka, kb);
+    load2_as_f32<DT>(p.new_v, row * p.nv_ts + (int64_t)h * p.nv_hs + d0, va, vb);
+    const int64_t slot = p.new_slot[row];
+    if (slot < 0) return;  // uniform
+    const Q8Pair rk = q8_quantize_pair(ka, kb);
+    const Q8Pair rv = q8_quantize_pair(va, vb);
+    const int64_t page = slot / p.block_size;
+    const int off = (int)(slot - page * p.block_size);
+    const int64_t sub = (int64_t)(off >> 4) * SUBPAGE_BYTES;
+    planar_store_pair(const_cast<uint8_t *>(p.kc) + page * p.cbs + (int64_t)h * p.chs + sub,
+                      const_cast<uint8_t *>(p.vc) + page * p.vcbs + (int64_t)h * p.vchs + sub, off & 15, lane,
+                      rk, rv);
+}
+
 constexpr int DEC_NW = 4;          // waves per decode workgroup
 constexpr int DEC_MIN_UNITS = 16;  // sub-pages per decode workgroup, at least
 
@@ -489,6 +517,46 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     s = __builtin_amdgcn_readfirstlane(s);
     Ps = uniform64(Ps);
     SegInfo si = seg_info(p, s);
+
+    if (p.new_k) {
+        // Fused cache write, before any streaming: the walk of the main loop
+        // below over this workgroup's pieces.  The step's new tokens (positions
+        // sl - n_q .. sl - 1, input rows q0 ..) that lie in a piece's
+        // sub-pages are quantized and stored by the wave that will stream
+        // their sub-page (wave (js - a) % DEC_NW takes sub-page js of piece
+        // [a, b)), so each new (token, kv-head) is written once, by the only
+        // wave that reads it in this launch, and that wave's later loads
+        // follow its own stores in program order.
+        int64_t uu = u0, Pw = Ps;
+        int sw = s;
+        SegInfo sv = si;
+        while (uu < u1) {
+            const int64_t off = uu - Pw * Hkv;
+            const int hh = (int)(off / sv.nsub);
+            const int a = (int)(off - (int64_t)hh * sv.nsub);
+            const int b = (int)min((int64_t)sv.nsub, a + (u1 - uu));
+            const int lo = sv.sl - sv.nq;
+            for (int js = max(a, lo >> 4); js < b; ++js) {  // uniform
+                if (((js - a) & (DEC_NW - 1)) != wv) continue;
+                const int t_hi = min(16 * js + 16, sv.sl);
+                for (int pos = max(16 * js, lo); pos < t_hi; ++pos)
+                    write_new_token<QDT>(p, hh, sv.q0 + (pos - lo), lane);
+            }
+            uu += b - a;
+            if (uu < u1 && b == sv.nsub && hh == Hkv - 1) {
+                Pw += sv.nsub;
+                do {
+                    ++sw;
+                    sv = seg_info(p, sw);
+                } while (sv.nsub == 0 && sw + 1 < B);
+            }
+        }
+        // the stores above and this wave's loads of the same sub-pages below
+        // (other lanes of the same wave): a wavefront's memory operations are
+        // performed in order, so this fence costs no instruction; it keeps
+        // the compiler from moving the loads above the stores
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
 
     __shared__ float sm_o[DEC_NW][R][128 + 4];
     __shared__ float sm_m[DEC_NW][R], sm_l[DEC_NW][R];
@@ -1323,7 +1391,17 @@ extern "C" size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int
     return make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1)).bytes;
 }
 
-extern "C" hipError_t gfx906_fa_amd_paged_attention(
+namespace {
+
+// The step's new K/V rows for the fused cache write (element strides).
+struct NewKV {
+    const void *key, *value;
+    int dtype;
+    int64_t kts, khs, vts, vhs;
+    const int64_t *slot_mapping;
+};
+
+hipError_t paged_attention_impl(
     const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
     const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
     int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
@@ -1331,7 +1409,18 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
     int block_size, int max_query_len, int max_seq_len, float scale, void *out, int out_dtype,
     int64_t out_token_stride, int64_t out_head_stride, void *workspace, size_t workspace_bytes,
-    hipStream_t stream) {
+    const NewKV *nkv, hipStream_t stream) {
+    if (nkv && num_tokens > 0) {
+        const uint64_t align = nkv->dtype == GFA_DTYPE_F32 ? 8 : 4;  // two values per lane
+        if (nkv->dtype != q_dtype ||
+            (((uintptr_t)nkv->key | (uintptr_t)nkv->value) & (align - 1)) ||
+            ((uint64_t)(nkv->kts | nkv->khs | nkv->vts | nkv->vhs) & 1u)) {
+            fprintf(stderr,
+                    "[gfx906_fa_amd] paged_attention_kv_write: new key/value must have the query dtype, "
+                    "%d-byte aligned bases and even element strides\n", (int)align);
+            return hipErrorInvalidValue;
+        }
+    }
     if (num_seqs == 0 || num_tokens == 0) return hipSuccess;
     if (head_size != 128) {
         fprintf(stderr, "[gfx906_fa_amd] paged_attention: head_size=%d unsupported (only 128)\n", head_size);
@@ -1398,6 +1487,29 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
     p.ws_ml = nullptr;
     p.ws_o = nullptr;
     p.nwg = 0;
+    p.new_k = p.new_v = nullptr;
+    p.nk_ts = p.nk_hs = p.nv_ts = p.nv_hs = 0;
+    p.new_slot = nullptr;
+    if (nkv) {
+        if (q_abs_offset == nullptr && !pl.need_prefill) {
+            // every sequence is decode-shaped: its new tokens are the last n_q
+            // positions, written by the decode wave that streams their sub-page
+            p.new_k = nkv->key;
+            p.new_v = nkv->value;
+            p.nk_ts = nkv->kts;
+            p.nk_hs = nkv->khs;
+            p.nv_ts = nkv->vts;
+            p.nv_hs = nkv->vhs;
+            p.new_slot = nkv->slot_mapping;
+        } else {
+            // prefill rows read new tokens from many workgroups: write first
+            const hipError_t e = gfx906_fa_amd_cache_write_kv(
+                nkv->key, nkv->value, nkv->dtype, nkv->slot_mapping, const_cast<uint8_t *>(k_cache),
+                const_cast<uint8_t *>(v_cache), num_tokens, num_kv_heads, head_size, block_size, nkv->kts,
+                nkv->khs, nkv->vts, nkv->vhs, cache_block_stride, cache_head_stride, stream);
+            if (e != hipSuccess) return e;
+        }
+    }
 
 #define GFA_DISPATCH_O(QDT)                                                                    \
     switch (out_dtype) {                                                                       \
@@ -1411,6 +1523,50 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
         default: GFA_DISPATCH_O(GFA_DTYPE_BF16);
     }
 #undef GFA_DISPATCH_O
+}
+
+}  // namespace
+
+extern "C" hipError_t gfx906_fa_amd_paged_attention(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
+    int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *q_abs_offset,
+    int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
+    int block_size, int max_query_len, int max_seq_len, float scale, void *out, int out_dtype,
+    int64_t out_token_stride, int64_t out_head_stride, void *workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+    return paged_attention_impl(q, q_dtype, q_token_stride, q_head_stride, k_cache, v_cache,
+                                cache_block_stride, cache_head_stride, block_table, block_table_stride,
+                                seq_lens, query_start_loc, q_abs_offset, causal, num_seqs, num_tokens,
+                                num_heads, num_kv_heads, head_size, block_size, max_query_len, max_seq_len,
+                                scale, out, out_dtype, out_token_stride, out_head_stride, workspace,
+                                workspace_bytes, nullptr, stream);
+}
+
+extern "C" hipError_t gfx906_fa_amd_paged_attention_kv_write(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
+    int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *q_abs_offset,
+    int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
+    int block_size, int max_query_len, int max_seq_len, float scale, void *out, int out_dtype,
+    int64_t out_token_stride, int64_t out_head_stride, void *workspace, size_t workspace_bytes,
+    const void *key, const void *value, int kv_dtype, int64_t key_token_stride,
+    int64_t key_head_stride, int64_t value_token_stride, int64_t value_head_stride,
+    const int64_t *slot_mapping, hipStream_t stream) {
+    if (key == nullptr || value == nullptr || slot_mapping == nullptr) {
+        fprintf(stderr, "[gfx906_fa_amd] paged_attention_kv_write: key, value and slot_mapping are required\n");
+        return hipErrorInvalidValue;
+    }
+    const NewKV nkv{key, value, kv_dtype, key_token_stride, key_head_stride, value_token_stride,
+                    value_head_stride, slot_mapping};
+    return paged_attention_impl(q, q_dtype, q_token_stride, q_head_stride, k_cache, v_cache,
+                                cache_block_stride, cache_head_stride, block_table, block_table_stride,
+                                seq_lens, query_start_loc, q_abs_offset, causal, num_seqs, num_tokens,
+                                num_heads, num_kv_heads, head_size, block_size, max_query_len, max_seq_len,
+                                scale, out, out_dtype, out_token_stride, out_head_stride, workspace,
+                                workspace_bytes, &nkv, stream);
 }
 
 extern "C" hipError_t gfx906_fa_amd_paged_attention_tiled(

@@ -133,6 +133,30 @@ __device__ __forceinline__ uint16_t f32_to_half_bits(float d) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
+// Stores the Q8_0 K and V values a lane holds of one token row (columns
+// d0 = 2*lane and d0+1, from q8_quantize_pair) into a planar K and V
+// sub-page at token tt, plus the block scales from the first lane of each
+// 16-lane row:
+//   K ints  at (b/2)*1024 + (4tt + g)*16 + (b%2)*8 + d%8   (b = d/32, g = (d%32)/8)
+//   V ints  at (m/4)*1024 + ((tt/4)*16 + d%16)*16 + (m%4)*4 + tt%4   (m = d/16)
+//   scales  K at 2048 + (4tt + b)*2, V at 2048 + ((tt/4)*4 + b)*8 + (tt%4)*2
+__device__ __forceinline__ void planar_store_pair(uint8_t *ksub, uint8_t *vsub, int tt, int lane,
+                                                  const Q8Pair &rk, const Q8Pair &rv) {
+    const int d0 = 2 * lane;
+    const int b = lane >> 4;
+    const int kpos = (b >> 1) * 1024 + (4 * tt + ((d0 >> 3) & 3)) * 16 + (b & 1) * 8 + (d0 & 7);
+    *reinterpret_cast<uint16_t *>(ksub + kpos) = (uint16_t)((uint8_t)rk.qa | ((uint16_t)(uint8_t)rk.qb << 8));
+    const int m = d0 >> 4;
+    const int vrow = (m >> 2) * 1024 + ((tt >> 2) * 16) * 16 + (m & 3) * 4 + (tt & 3);
+    vsub[vrow + (d0 & 15) * 16] = (uint8_t)rv.qa;
+    vsub[vrow + ((d0 + 1) & 15) * 16] = (uint8_t)rv.qb;
+    if ((lane & 15) == 0) {
+        *reinterpret_cast<uint16_t *>(ksub + SCALE_OFF + (4 * tt + b) * 2) = f32_to_half_bits(rk.d);
+        *reinterpret_cast<uint16_t *>(vsub + SCALE_OFF + ((tt >> 2) * 4 + b) * 8 + (tt & 3) * 2) =
+            f32_to_half_bits(rv.d);
+    }
+}
+
 // 4 int8 (one dword) -> 4 exact fp16 values as two packed pairs.
 // u = q ^ 0x80 is q + 128 as an unsigned byte; fp16 bits 0x6400|u encode
 // 1024 + u exactly, and subtracting 1152 leaves q exactly.

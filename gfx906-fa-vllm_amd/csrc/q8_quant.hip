@@ -122,21 +122,7 @@ __global__ __launch_bounds__(256) void q8_cache_write_kv_kernel(
     const int64_t base = page * cbs + (int64_t)h * chs + (int64_t)sp * SUBPAGE_BYTES;
     const Q8Pair rk = q8_quantize_pair(ka, kb);
     const Q8Pair rv = q8_quantize_pair(va, vb);
-
-    const int b = lane >> 4;
-    const int kb2 = d0 >> 5, kg = (d0 >> 3) & 3;
-    const int kpos = (kb2 >> 1) * 1024 + (4 * tt + kg) * 16 + (kb2 & 1) * 8 + (d0 & 7);
-    *reinterpret_cast<uint16_t *>(kc + base + kpos) =
-        (uint16_t)((uint8_t)rk.qa | ((uint16_t)(uint8_t)rk.qb << 8));
-    const int m = d0 >> 4;
-    const int vrow = (m >> 2) * 1024 + ((tt >> 2) * 16) * 16 + (m & 3) * 4 + (tt & 3);
-    vc[base + vrow + (d0 & 15) * 16] = (uint8_t)rv.qa;
-    vc[base + vrow + ((d0 + 1) & 15) * 16] = (uint8_t)rv.qb;
-    if ((lane & 15) == 0) {
-        *reinterpret_cast<uint16_t *>(kc + base + SCALE_OFF + (4 * tt + b) * 2) = f32_to_half_bits(rk.d);
-        *reinterpret_cast<uint16_t *>(vc + base + SCALE_OFF + ((tt >> 2) * 4 + b) * 8 + (tt & 3) * 2) =
-            f32_to_half_bits(rv.d);
-    }
+    planar_store_pair(kc + base, vc + base, tt, lane, rk, rv);
 }
 
 // ---------------------------------------------------------------------------

@@ -77,6 +77,9 @@ def _load():
         "gfx906_fa_amd_paged_attention_workspace_size": (SZ, [I, I, I, I, I, I, I]),
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
+        "gfx906_fa_amd_paged_attention_kv_write": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
+                                                       I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ,
+                                                       P, P, I, I64, I64, I64, I64, P, P]),
         "gfx906_fa_amd_pack_flat_kv": (I, [P, P, P, P, I, I, I, P]),
         "gfx906_fa_amd_paged_attention_tiled": (I, [P, I, I64, I64, P, P, I, I64, I64, I64, I64, P, I64,
                                                     P, P, P, I, P, I64, I64, I, I, I, I, I, I, I, I,
@@ -376,11 +379,17 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
                     scale: float, out: Optional[torch.Tensor] = None,
                     workspace: Optional[torch.Tensor] = None,
                     q_abs_offset: Optional[torch.Tensor] = None, causal: bool = True,
-                    out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+                    out_dtype: Optional[torch.dtype] = None, new_key: Optional[torch.Tensor] = None,
+                    new_value: Optional[torch.Tensor] = None,
+                    slot_mapping: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Varlen direct-paged attention: query [T, Hq, 128] -> out [T, Hq, 128].
 
     ``max_query_len`` / ``max_seq_len`` must bound the device values (they
-    size the launch; they are host ints so no device sync is needed)."""
+    size the launch; they are host ints so no device sync is needed).
+    With ``new_key`` / ``new_value`` [T, Hkv, 128] (the query dtype) and
+    ``slot_mapping`` (int64 [T]) the step's K/V are first written to the cache
+    as ``reshape_and_cache_q8_kv`` does; decode-shaped batches do it inside
+    the attention launch."""
     for t, n in ((query, "query"), (block_table, "block_table"), (seq_lens, "seq_lens"),
                  (query_start_loc, "query_start_loc")):
         _cuda(t, n)
@@ -412,6 +421,28 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
         workspace = new_workspace(need, query.device)
     _check(workspace.data_ptr() % 256 == 0, "workspace must be 256-byte aligned")
     ws_bytes = workspace.numel() * workspace.element_size()
+    if new_key is not None or new_value is not None or slot_mapping is not None:
+        _check(new_key is not None and new_value is not None and slot_mapping is not None,
+               "new_key, new_value and slot_mapping go together")
+        for t, n in ((new_key, "new_key"), (new_value, "new_value"), (slot_mapping, "slot_mapping")):
+            _cuda(t, n)
+        _check(new_key.dtype == query.dtype and new_value.dtype == query.dtype,
+               "new_key / new_value must have the query dtype")
+        _check(new_key.dim() == 3 and new_value.shape == new_key.shape and new_key.shape[0] >= T
+               and tuple(new_key.shape[1:]) == (Hkv, D), "new_key / new_value must be [num_tokens, Hkv, 128]")
+        _check(new_key.stride(2) == 1 and new_value.stride(2) == 1, "new_key / new_value rows must be contiguous")
+        _check(slot_mapping.dtype == torch.int64 and slot_mapping.shape[0] >= T, "slot_mapping must be int64 [T]")
+        sm = slot_mapping.contiguous()
+        err = _load().gfx906_fa_amd_paged_attention_kv_write(
+            _ptr(query), _DT[query.dtype], query.stride(0), query.stride(1), _ptr(key_cache),
+            _ptr(value_cache), cbs, chs, _ptr(block_table), block_table.stride(0), _ptr(seq_lens),
+            _ptr(query_start_loc), _ptr(q_abs_offset), 1 if causal else 0, B, T, Hq, Hkv, D, bs,
+            int(max_query_len), int(max_seq_len), float(scale), _ptr(out), _DT[out.dtype],
+            out.stride(0), out.stride(1), _ptr(workspace), ws_bytes, _ptr(new_key), _ptr(new_value),
+            _DT[new_key.dtype], new_key.stride(0), new_key.stride(1), new_value.stride(0), new_value.stride(1),
+            _ptr(sm), _stream(query.device))
+        _ok(err, "gfx906_fa_amd_paged_attention_kv_write")
+        return out
     err = _load().gfx906_fa_amd_paged_attention(
         _ptr(query), _DT[query.dtype], query.stride(0), query.stride(1), _ptr(key_cache),
         _ptr(value_cache), cbs, chs, _ptr(block_table), block_table.stride(0), _ptr(seq_lens),

@@ -173,6 +173,22 @@ def sub_batch(b: Batch, s0: int, s1: int) -> Batch:
     return sb
 
 
+def rope_cos_sin_cache(max_position: int, rot_dim: int, dtype: torch.dtype, device,
+                       base: float = 10000.0) -> torch.Tensor:
+    """[max_position, rot_dim] table cos | sin of position * base^(-2i/rot_dim),
+    the layout of vLLM's rotary cos_sin_cache (synthetic bench input)."""
+    inv = 1.0 / (base ** (torch.arange(0, rot_dim, 2, dtype=torch.float32) / rot_dim))
+    f = torch.outer(torch.arange(max_position, dtype=torch.float32), inv)
+    return torch.cat([f.cos(), f.sin()], dim=-1).to(dtype).to(device)
+
+
+def rope_write_bytes(T: int, Hq: int, Hkv: int, D: int = 128, rot: int = 128, elem: int = 2) -> int:
+    """Algorithmic HBM bytes of the fused rotary + K/V cache write over T
+    tokens: query and key read and written back, value read, the Q8_0 K and
+    V rows written (2 x 136 B per kv-head), one cos/sin row, position and slot."""
+    return T * ((Hq + Hkv) * D * elem * 2 + Hkv * D * elem + Hkv * 2 * (D // 32 * 34) + rot * elem + 16)
+
+
 # ---------------------------------------------------------------------------
 # The benchmark configurations
 # ---------------------------------------------------------------------------

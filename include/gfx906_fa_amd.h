@@ -216,6 +216,34 @@ hipError_t gfx906_fa_amd_paged_attention(
     void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
     void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* (5b) (4) followed by (5) in one call: key / value [num_tokens, Hkv, D] (the
+ *      query dtype, element strides) are quantized to Q8_0 and written at
+ *      slot_mapping[t] (< 0 = skip) before attention reads the cache.  When
+ *      every sequence is decode-shaped (n_q*Hq/Hkv <= 32 rows) and
+ *      q_abs_offset is NULL, the new tokens are the last n_q positions of
+ *      their sequences and the decode kernel itself quantizes each one in the
+ *      wave that streams its sub-page, uses those bytes for attention and
+ *      stores them - one launch fewer per decode step; otherwise (4) runs
+ *      first.  The cache bytes and the output equal those of (4) then (5) on
+ *      the same inputs, provided slot_mapping puts each new token at its
+ *      position in block_table (as vLLM's metadata does).
+ *      Replaces the reference's do_kv_cache_update + forward pair for decode
+ *      steps (extension/gfx906_fa_backend.py:405-461), which the backend
+ *      issues as two launches.
+ */
+hipError_t gfx906_fa_amd_paged_attention_kv_write(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
+    int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *q_abs_offset,
+    int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
+    int head_size, int block_size, int max_query_len, int max_seq_len, float scale,
+    void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
+    void *workspace, size_t workspace_bytes, const void *key, const void *value,
+    int kv_dtype, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t *slot_mapping,
+    hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * (6) Repack the reference's contiguous attention inputs for (7):
  *       k_aos [rows, Skv, 136] AoS Q8_0 K rows -> k_planar [rows, Skv_pad/16, 2176]

@@ -21,11 +21,13 @@ DEV = "cuda"
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("heads,q_len", [((48, 8), 1), ((6, 1), 5)])
-def test_decode_step_graph_replay(heads, q_len):
+def test_decode_step_graph_replay(heads, q_len, fused):
+    """fused: the cache write folded into the attention call."""
     need_gpu()
     Hq, Hkv = heads
-    announce(f"graph replay heads={heads} q_len={q_len}")
+    announce(f"graph replay heads={heads} q_len={q_len} fused={fused}")
     B, bs, max_blocks = 8, 16, 48
     NB = B * max_blocks
     T = B * q_len
@@ -64,6 +66,10 @@ def test_decode_step_graph_replay(heads, q_len):
         return lens, table
 
     def step():
+        if fused:
+            gfx906_fa.paged_attention(q, kp, vp, bt, sl, qsl, q_len, max_blocks * bs, scale, out=out,
+                                      workspace=ws, new_key=k_new, new_value=v_new, slot_mapping=slots)
+            return
         gfx906_fa.reshape_and_cache_q8_kv(k_new, v_new, slots, kp, vp)
         gfx906_fa.paged_attention(q, kp, vp, bt, sl, qsl, q_len, max_blocks * bs, scale, out=out, workspace=ws)
 
