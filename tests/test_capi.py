@@ -55,6 +55,23 @@ def test_validation_errors_without_gpu():
                                           0, 0, 0, 0, 0, 0, None) == 1
     # empty work is a no-op success
     assert L.gfx906_fa_amd_quantize_q8_0(None, 1, None, 0, 128, None) == 0
+    # fused rotary + write: rot_dim 72 is not a multiple of 16 (neox); fp32 rows;
+    # a valid configuration with no tokens is a no-op
+    rope = L.gfx906_fa_amd_rope_cache_write_kv
+    args = [None, None, None, 1, None, None, 1, 128, 4096, 128, 1, None, None, None, 0, 8, 2, 128, 16,
+            0, 0, 0, 0, 0, 0, 0, 0, None]
+    assert rope(*args) == 0
+    bad = list(args)
+    bad[9] = 72
+    assert rope(*bad) == 1
+    bad = list(args)
+    bad[3] = 0
+    assert rope(*bad) == 1
+    # attention with the write folded in: key / value / slot_mapping are required
+    err = L.gfx906_fa_amd_paged_attention_kv_write(None, 1, 0, 0, None, None, 0, 0, None, 0, None, None,
+                                                   None, 1, 1, 1, 8, 1, 128, 16, 1, 16, 0.1, None, 1, 0,
+                                                   0, None, 0, None, None, 1, 0, 0, 0, 0, None, None)
+    assert err == 1
 
 
 def test_workspace_size_plan():
