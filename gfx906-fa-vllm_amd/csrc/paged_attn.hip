@@ -755,9 +755,9 @@ constexpr int PF_KPITCH = 272;
 constexpr int PF_VPITCH = 2 * PF_TK + 16;
 constexpr int PF_KBYTES = PF_TK * PF_KPITCH;
 constexpr int PF_VBYTES = 128 * PF_VPITCH;
-constexpr int PF_STAGE = PF_KBYTES + PF_VBYTES;
 
 typedef float float16v_t __attribute__((ext_vector_type(16)));
+typedef uint64_t u64x8_t __attribute__((ext_vector_type(8)));
 struct PHalf8 {
     half2_t h[4];
 };
@@ -808,67 +808,67 @@ __device__ __forceinline__ half2_t finite2(half2_t x) {
     return __builtin_elementwise_min(__builtin_elementwise_max(x, -hi), hi);
 }
 
-// Dequantizes the lane's raw half sub-page into the LDS stage (sub-page sp of
-// the tile).  TAIL (the last tile of the range, the only one that can hold
-// keys past kv_end): bytes of tokens past the valid range are dequantized as
-// they are - their scores are masked to -inf (P = 0) - and the V scales are
-// made finite so that 0 * V^ stays 0.
+// Dequantizes the lane's raw half sub-page into the LDS stages (sub-page sp
+// of the tile): K^ rows into kst, V^T columns into vst.  TAIL (the last tile
+// of the range, the only one that can hold keys past kv_end): bytes of tokens
+// past the valid range are dequantized as they are - their scores are masked
+// to -inf (P = 0) - and the V scales are made finite so that 0 * V^ stays 0.
+__device__ __forceinline__ void pf_dequant_k(const PfRaw &r, uint8_t *kst, int sp, int lane, int hf) {
+    const int t = lane & 15, g = lane >> 4;
+    // (vector elements are copied to scalars before __builtin_bit_cast: a
+    // bit_cast of an ext_vector element lvalue reads element 0 with this clang)
+    const half2_t ks = __builtin_bit_cast(half2_t, r.ks);
+    const uint32_t k0 = r.k[0], k1 = r.k[1], k2 = r.k[2], k3 = r.k[3];
+    // K^: row 16sp + t, d chunks 4b + g (8 fp16 each)
+    uint8_t *krow = kst + (16 * sp + t) * PF_KPITCH + 16 * g + 128 * hf;
+    *reinterpret_cast<half8_t *>(krow) = scale8(i8x8_to_half8(k0, k1), ks[0]);
+    *reinterpret_cast<half8_t *>(krow + 64) = scale8(i8x8_to_half8(k2, k3), ks[1]);
+}
+
 template <bool TAIL, bool VF16>
-__device__ __forceinline__ void pf_dequant(const PfRaw &r, uint8_t *stage, int sp, int lane, int hf) {
-    {
-        const int t = lane & 15, g = lane >> 4;
-        // (vector elements are copied to scalars before __builtin_bit_cast: a
-        // bit_cast of an ext_vector element lvalue reads element 0 with this clang)
-        const half2_t ks = __builtin_bit_cast(half2_t, r.ks);
-        const uint32_t k0 = r.k[0], k1 = r.k[1], k2 = r.k[2], k3 = r.k[3];
-        // K^: row 16sp + t, d chunks 4b + g (8 fp16 each)
-        uint8_t *krow = stage + (16 * sp + t) * PF_KPITCH + 16 * g + 128 * hf;
-        *reinterpret_cast<half8_t *>(krow) = scale8(i8x8_to_half8(k0, k1), ks[0]);
-        *reinterpret_cast<half8_t *>(krow + 64) = scale8(i8x8_to_half8(k2, k3), ks[1]);
-    }
-    {
-        const int i = lane & 15, T = lane >> 4;
-        const uint32_t vq[4] = {r.v[0], r.v[1], r.v[2], r.v[3]};
-        const uint32_t vsw[4] = {r.vs[0], r.vs[1], r.vs[2], r.vs[3]};
-        // V^T: rows d = i + 16m; the 4 tokens 4T..4T+3 of sub-page sp sit at
-        // contraction position 16sp + 8(T&1) + 4(T>>1) (key bits 2 and 3 swapped)
-        uint8_t *vcol = stage + PF_KBYTES + (i + 64 * hf) * PF_VPITCH +
-                        2 * (16 * sp + 8 * (T & 1) + 4 * (T >> 1));
-        if constexpr (VF16) {  // already fp16: 4 tokens of d = i + 16(4hf + mm) per 8 bytes
-#pragma unroll
-            for (int mm = 0; mm < 4; ++mm) {
-                const uint32_t lo = mm < 2 ? vq[2 * mm] : vsw[2 * mm - 4];
-                const uint32_t hi = mm < 2 ? vq[2 * mm + 1] : vsw[2 * mm - 3];
-                *reinterpret_cast<u32x2 *>(vcol + 16 * mm * PF_VPITCH) = u32x2{lo, hi};
-            }
-            return;
-        }
+__device__ __forceinline__ void pf_dequant_v(const PfRaw &r, uint8_t *vst, int sp, int lane, int hf) {
+    const int i = lane & 15, T = lane >> 4;
+    const uint32_t vq[4] = {r.v[0], r.v[1], r.v[2], r.v[3]};
+    const uint32_t vsw[4] = {r.vs[0], r.vs[1], r.vs[2], r.vs[3]};
+    // V^T: rows d = i + 16m; the 4 tokens 4T..4T+3 of sub-page sp sit at
+    // contraction position 16sp + 8(T&1) + 4(T>>1) (key bits 2 and 3 swapped)
+    uint8_t *vcol = vst + (i + 64 * hf) * PF_VPITCH + 2 * (16 * sp + 8 * (T & 1) + 4 * (T >> 1));
+    if constexpr (VF16) {  // already fp16: 4 tokens of d = i + 16(4hf + mm) per 8 bytes
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) {
-            const int b = mm >> 1;  // block 2hf + b: scale dwords 2b (tokens 0,1), 2b+1 (2,3)
-            half2_t s01 = __builtin_bit_cast(half2_t, vsw[2 * b]);
-            half2_t s23 = __builtin_bit_cast(half2_t, vsw[2 * b + 1]);
-            if (TAIL) {
-                s01 = finite2(s01);
-                s23 = finite2(s23);
-            }
-            half2_t lo, hi;
-            i8x4_to_f16x4(vq[mm], lo, hi);
-            lo *= s01;
-            hi *= s23;
-            *reinterpret_cast<half4_t *>(vcol + 16 * mm * PF_VPITCH) = half4_t{lo[0], lo[1], hi[0], hi[1]};
+            const uint32_t lo = mm < 2 ? vq[2 * mm] : vsw[2 * mm - 4];
+            const uint32_t hi = mm < 2 ? vq[2 * mm + 1] : vsw[2 * mm - 3];
+            *reinterpret_cast<u32x2 *>(vcol + 16 * mm * PF_VPITCH) = u32x2{lo, hi};
         }
+        return;
+    }
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        const int b = mm >> 1;  // block 2hf + b: scale dwords 2b (tokens 0,1), 2b+1 (2,3)
+        half2_t s01 = __builtin_bit_cast(half2_t, vsw[2 * b]);
+        half2_t s23 = __builtin_bit_cast(half2_t, vsw[2 * b + 1]);
+        if (TAIL) {
+            s01 = finite2(s01);
+            s23 = finite2(s23);
+        }
+        half2_t lo, hi;
+        i8x4_to_f16x4(vq[mm], lo, hi);
+        lo *= s01;
+        hi *= s23;
+        *reinterpret_cast<half4_t *>(vcol + 16 * mm * PF_VPITCH) = half4_t{lo[0], lo[1], hi[0], hi[1]};
     }
 }
 
 template <int QDT, int ODT, bool VF16, bool MASK>
 __global__ __launch_bounds__(64 * PF_WAVES)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p) {
-    // two LDS stages as distinct objects: the compiler can then prove that
-    // the dequant stores (one stage) and the MFMA operand reads (the other)
-    // are independent and interleave them
-    __shared__ __attribute__((aligned(16))) uint8_t lds0[PF_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t lds1[PF_STAGE];
+    // two LDS stages of K^ and of V^, each a distinct object: the compiler
+    // can then prove that the dequant stores (one stage) and the MFMA operand
+    // reads (the other) are independent and interleave them
+    __shared__ __attribute__((aligned(16))) uint8_t ldsk0[PF_KBYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsk1[PF_KBYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsv0[PF_VBYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsv1[PF_VBYTES];
     const int Hkv = p.Hkv;
     const int h = blockIdx.x % Hkv;
     int s, rt;
@@ -959,10 +959,14 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         pf_fetch<VF16>(rw.h[0], kb, vb, lane, hf);
         if constexpr (PF_NSP == 8) pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
     };
-    auto dequant = [&](const PfRawT &rw, uint8_t *st, auto tail) {
+    auto dequant_k = [&](const PfRawT &rw, uint8_t *kst) {
+        pf_dequant_k(rw.h[0], kst, wsp, lane, hf);
+        if constexpr (PF_NSP == 8) pf_dequant_k(rw.h[1], kst, wsp, lane, 1);
+    };
+    auto dequant_v = [&](const PfRawT &rw, uint8_t *vst, auto tail) {
         constexpr bool T = decltype(tail)::value;
-        pf_dequant<T, VF16>(rw.h[0], st, wsp, lane, hf);
-        if constexpr (PF_NSP == 8) pf_dequant<T, VF16>(rw.h[1], st, wsp, lane, 1);
+        pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, hf);
+        if constexpr (PF_NSP == 8) pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
     };
 
     float16v_t o[4];
@@ -971,17 +975,14 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
     // Running max m (log2 units) enters the S MFMA chain as its accumulator
-    // input (-m in all 16 lanes of cneg), so S' = S - m comes out of the
-    // matrix core directly.  has_m: a visible key has been seen (m valid).
+    // input (-m in all 16 registers), so S' = S - m comes out of the matrix
+    // core directly.  has_m: a visible key has been seen (m valid).
     float m_use = 0.0f, l_run = 0.0f;
     bool has_m = false;
-    float16v_t cneg;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) cneg[e] = 0.0f;
 
     // lane-constant LDS offsets of the MFMA operands
     const int kread = (lane & 31) * PF_KPITCH + 16 * hb;            // + 32*st*KPITCH + 32*kk
-    const int vread = PF_KBYTES + (lane & 31) * PF_VPITCH + 16 * hb;  // + 32*dt*VPITCH + 16*(4st+2sg)
+    const int vread = (lane & 31) * PF_VPITCH + 16 * hb;  // + 32*dt*VPITCH + 16*(4st+2sg)
 
     // One pipeline step: loads of tile kt+2 into rf, dequant of tile kt+1
     // from rd, attention over tile kt.
@@ -989,23 +990,36 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     //       1 = same, tile kt+1 being the last (tail) tile,
     //       2 = nothing left to fetch or dequantize
     auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode) {
-        // odd: kt & 1 (compile time) - read stage kt&1, write stage (kt+1)&1
-        const uint8_t *stage = decltype(odd)::value ? lds1 : lds0;
-        uint8_t *wstage = decltype(odd)::value ? lds0 : lds1;
+        // odd: kt & 1 (compile time) - read stages kt&1, write stages (kt+1)&1
+        const uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
+        const uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
+        uint8_t *wkst = decltype(odd)::value ? ldsk0 : ldsk1;
+        uint8_t *wvst = decltype(odd)::value ? ldsv0 : ldsv1;
         constexpr int MODE = decltype(mode)::value;
+        using TailV = std::integral_constant<bool, MODE == 1>;
         if constexpr (MODE != 2) {
             fetch(rf, kt + 2);
-            dequant(rd, wstage, std::integral_constant<bool, MODE == 1>{});
+            dequant_k(rd, wkst);
+            dequant_v(rd, wvst, TailV{});
         }
 
         // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile
         float16v_t sacc[PF_NST];
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
-            sacc[st] = cneg;
+            {   // -m in all 16 accumulator registers, built as a 64-bit splat:
+                // the compiler then builds it once per tile, feeds it to the
+                // first MFMA of both chains as srcC and keeps the kernel
+                // spill-free (a float splat was rebuilt per chain, 32 moves)
+                const uint64_t pr = ((uint64_t)__float_as_uint(-m_use) << 32) | __float_as_uint(-m_use);
+                u64x8_t sp;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sp[e] = pr;
+                sacc[st] = __builtin_bit_cast(float16v_t, sp);
+            }
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
-                const half8_t a = *reinterpret_cast<const half8_t *>(stage + kread + 32 * st * PF_KPITCH + 32 * kk);
+                const half8_t a = *reinterpret_cast<const half8_t *>(kst + kread + 32 * st * PF_KPITCH + 32 * kk);
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
@@ -1052,8 +1066,6 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
             for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
 #pragma unroll
             for (int st = 0; st < PF_NST; ++st) sacc[st] -= delta;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) cneg[e] = -m_use;
         }
         // Row sum of the fp16-rounded p with v_dot2 (the same values the PV
         // MFMAs consume).  v_dot2 issues to the matrix pipe; plain fp32 adds
@@ -1077,7 +1089,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) {
                     const half8_t a = *reinterpret_cast<const half8_t *>(
-                        stage + vread + 32 * dt * PF_VPITCH + 16 * (4 * st + 2 * sg));
+                        vst + vread + 32 * dt * PF_VPITCH + 16 * (4 * st + 2 * sg));
                     o[dt] = mfma32(a, pb, o[dt]);
                 }
             }
@@ -1097,11 +1109,12 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         ready(pw0);
         ready(pw1);
         fetch(r0, 0);
+        dequant_k(r0, ldsk0);
         if (ntk > 1) {
             fetch(r1, 1);
-            dequant(r0, lds0, std::integral_constant<bool, false>{});
+            dequant_v(r0, ldsv0, std::integral_constant<bool, false>{});
         } else {
-            dequant(r0, lds0, std::integral_constant<bool, true>{});
+            dequant_v(r0, ldsv0, std::integral_constant<bool, true>{});
         }
     }
     __syncthreads();

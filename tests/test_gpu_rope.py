@@ -74,6 +74,31 @@ def test_rope_cache_write_bitexact(dt, neox, rot, cs_dtype):
     assert np.array_equal(cache.cpu().numpy(), exp)
 
 
+@pytest.mark.parametrize("heads", [(6, 1), (4, 4), (40, 8)])
+def test_rope_head_counts(heads):
+    """Head counts whose query and key rows share a 4-row iteration of a
+    wave (6/1: rows 4, 5 query, 6 key), equal counts, and more than one
+    32-row chunk per token."""
+    need_gpu()
+    Hq, Hkv = heads
+    announce(f"rope heads {Hq}/{Hkv}")
+    T, bs, NB = 45, 16, 4
+    qkv, cs_t, cs, pos_t, pos = _case("f16", T, Hq, Hkv, 128, "model", seed=Hq * 7 + Hkv)
+    q, k, v = qkv[:, :Hq], qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
+    q0, k0, v0 = host_bits(q.contiguous()), host_bits(k.contiguous()), host_bits(v.contiguous())
+    slots = np.random.default_rng(3).permutation(NB * bs)[:T].astype(np.int64)
+    cache = torch.zeros((NB, 2, Hkv, bs // 16 * 2176), dtype=torch.uint8, device=DEV)
+    gfx906_fa.rope_and_cache_q8_kv(pos_t, q, k, v, cs_t, True, torch.from_numpy(slots).to(DEV),
+                                   cache[:, 0], cache[:, 1])
+    torch.cuda.synchronize()
+    kr = O.rope_ref(k0, pos, cs, 128, True)
+    assert np.array_equal(host_bits(q.contiguous()), O.rope_ref(q0, pos, cs, 128, True))
+    assert np.array_equal(host_bits(k.contiguous()), kr)
+    exp = np.zeros(tuple(cache.shape), np.uint8)
+    O.planar_cache_write(kr, v0, slots, exp)
+    assert np.array_equal(cache.cpu().numpy(), exp)
+
+
 def _torch_rope_(x, positions, cos_sin, rot, neox):
     """vLLM's native rotary form with torch ops, written back into x."""
     cs = cos_sin[positions]
