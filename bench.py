@@ -16,7 +16,10 @@ Also reported on the same JSON line:
   roofline      - attention pass (decode + split combine) algorithmic bytes /
                   its average duration from HIP events on the launch stream,
                   against 8 TB/s; ``traffic`` from the committed rocprofv3
-                  FETCH_SIZE/WRITE_SIZE measurement when present.
+                  FETCH_SIZE/WRITE_SIZE measurement when present;
+                  ``copy_ceiling_gbs`` a plain 1 GiB device copy (read + write
+                  bytes / time) on the same GPU, and ``frac_of_copy`` the
+                  attention rate against it.
   prefill       - cfg3 (32K causal prefill, bf16, 48/8): attention TFLOP/s
                   (4*D*Hq*sum of visible keys) vs 2.5 PFLOP/s dense fp16/bf16
                   MFMA peak, the K/V quantize-write GB/s, and the fused
@@ -226,6 +229,14 @@ def main() -> int:
     ms_step = timed(step, args.steps, args.warmup)
     ms_attn = timed(attn, args.steps, args.warmup)
 
+    # the measured ceiling of a plain streaming kernel on this part: torch's
+    # device copy of 1 GiB, read + write bytes over its time
+    csrc = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    cdst = torch.empty_like(csrc)
+    ms_copy = timed(lambda: cdst.copy_(csrc), 20, 5)
+    copy_gbs = 2 * csrc.numel() * 4 / (ms_copy * 1e-3) / 1e9
+    del csrc, cdst
+
     step_bytes = b.hbm_bytes(out_bytes_per_elem=2) + B * b.Hkv * (2 * 2 * 128 + 2 * 136) + B * 8
     attn_bytes = b.hbm_bytes(out_bytes_per_elem=2)
     value = step_bytes / (ms_step * 1e-3) / 1e9
@@ -256,6 +267,7 @@ def main() -> int:
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic, "algorithmic_bytes": attn_bytes, "avg_us": round(ms_attn * 1e3, 2),
+            "copy_ceiling_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4),
         },
     }
 
