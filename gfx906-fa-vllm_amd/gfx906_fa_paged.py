@@ -16,6 +16,8 @@ planes (``q8_planes``).
 from __future__ import annotations
 
 import math
+import os
+import time
 from typing import Optional, Tuple
 
 import torch
@@ -24,6 +26,25 @@ import gfx906_fa
 
 SUBPAGE_TOKENS = gfx906_fa.SUBPAGE_TOKENS
 SUBPAGE_BYTES = gfx906_fa.SUBPAGE_BYTES
+
+# GFX906_FA_FWD_DEBUG=1: one line per forward_paged call (shapes before the
+# launch, then OK or FAILED with the error) appended to
+# /tmp/gfx906_fa_debug/fwd-<pid>.log, with the device synchronized around the
+# launch so an asynchronous fault is reported by the call that caused it
+# (extension/gfx906_fa_paged.py:23,72-80,297-320).
+_DBG = os.environ.get("GFX906_FA_FWD_DEBUG", "0") == "1"
+_DBG_DIR = "/tmp/gfx906_fa_debug"
+
+
+def _fwdlog(msg: str) -> None:
+    if not _DBG:
+        return
+    try:
+        os.makedirs(_DBG_DIR, exist_ok=True)
+        with open(os.path.join(_DBG_DIR, f"fwd-{os.getpid()}.log"), "a") as f:
+            f.write(f"[{time.time():.3f}] {msg}\n")
+    except OSError:
+        pass
 
 
 def plane_bytes_per_head(block_size: int) -> int:
@@ -120,7 +141,22 @@ def forward_paged(
     o3 = None
     if out is not None:
         o3 = out.view(out.shape[0], Hq, D)
-    res = gfx906_fa.paged_attention(query, key_cache, value_cache, bt, sl.contiguous(), cu.contiguous(),
-                                    max_seqlen_q, max_seqlen_k, scale, out=o3, workspace=workspace,
-                                    out_dtype=torch.float32)
+    if _DBG:
+        _fwdlog(f"forward_paged VARLEN: num_tokens={num_tokens} Hq={Hq} Hkv={key_cache.shape[1]} D={D} "
+                f"num_seqs={sl.shape[0]} Sq_max={max_seqlen_q} Sk_max={max_seqlen_k} "
+                f"q_dtype={query.dtype} out={None if out is None else (tuple(out.shape), out.dtype)} "
+                f"scale={scale}")
+        if query.is_cuda:
+            torch.cuda.synchronize(query.device)
+    try:
+        res = gfx906_fa.paged_attention(query, key_cache, value_cache, bt, sl.contiguous(), cu.contiguous(),
+                                        max_seqlen_q, max_seqlen_k, scale, out=o3, workspace=workspace,
+                                        out_dtype=torch.float32)
+        if _DBG:
+            if query.is_cuda:
+                torch.cuda.synchronize(query.device)
+            _fwdlog(f"forward_paged OK: out={tuple(res.shape)}")
+    except Exception as e:
+        _fwdlog(f"forward_paged FAILED: {e!r}")
+        raise
     return res.view(res.shape[0], Hq * D)

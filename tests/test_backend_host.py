@@ -4,6 +4,8 @@ Follows tests/test_backend.py:30-57 of the reference (registration as
 CUSTOM, kv-cache shape equal to Triton's) and the error behaviour of
 extension/gfx906_fa_backend.py:247-257, 463-468.  vLLM itself is absent, so
 vLLM-side behaviour is unpinned; these tests pin this backend's side."""
+import os
+
 import pytest
 import torch
 
@@ -148,3 +150,33 @@ def test_graph_support_and_workspace_bound():
             for Hq, Hkv in ((48, 8), (6, 1), (32, 32)):
                 for mq in (1, 4, 5, 16, 2048):
                     assert gfx906_fa.workspace_size(n, n * mq, Hq, Hkv, mq, 1 << 17) <= bound
+
+
+def test_forward_debug_log_records_the_call_and_its_failure(tmp_path, monkeypatch):
+    """GFX906_FA_FWD_DEBUG: the call's shapes are logged before the launch and
+    the error after it, and the error still propagates.  CPU tensors make the
+    op fail its device check, so no GPU is needed."""
+    import os
+    import gfx906_fa_paged as P
+    monkeypatch.setattr(P, "_DBG", True)
+    monkeypatch.setattr(P, "_DBG_DIR", str(tmp_path / "dbg"))
+    q = torch.zeros(2, 8, 128, dtype=torch.float16)
+    kp = torch.zeros(4, 2, 2176, dtype=torch.uint8)
+    bt = torch.zeros(2, 1, dtype=torch.int32)
+    sl = torch.ones(2, dtype=torch.int32)
+    cu = torch.tensor([0, 1, 2], dtype=torch.int32)
+    with pytest.raises(RuntimeError):
+        P.forward_paged(q, kp, kp, bt, sl, cu, 1, 1)
+    lines = (tmp_path / "dbg" / f"fwd-{os.getpid()}.log").read_text().splitlines()
+    assert len(lines) == 2
+    assert "forward_paged VARLEN: num_tokens=2 Hq=8 Hkv=2 D=128 num_seqs=2" in lines[0]
+    assert "forward_paged FAILED" in lines[1]
+
+
+def test_forward_debug_log_off_by_default(tmp_path, monkeypatch):
+    import gfx906_fa_paged as P
+    assert P._DBG == (os.environ.get("GFX906_FA_FWD_DEBUG", "0") == "1")
+    monkeypatch.setattr(P, "_DBG", False)
+    monkeypatch.setattr(P, "_DBG_DIR", str(tmp_path / "dbg"))
+    P._fwdlog("x")
+    assert not (tmp_path / "dbg").exists()

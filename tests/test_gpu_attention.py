@@ -82,6 +82,42 @@ def test_decode_block_sizes(bs):
     _run_and_check(b)
 
 
+@pytest.mark.parametrize("bs", [128, 256])
+def test_mixed_batch_large_blocks(bs):
+    """Pages of 8 and 16 sub-pages, through both the decode and the prefill
+    kernel (vLLM's block size is any multiple of 16)."""
+    need_gpu()
+    b = W.build_batch([5, 300, 1500, 700, 33], [1, 1, 1, 300, 33], 12, 2, block_size=bs, seed=31)
+    _run_and_check(b)
+
+
+@pytest.mark.parametrize("nq", [1, 2, 3])
+def test_gqa_16(nq):
+    """G = 16 (64/4 heads): one query token fills the 16-row decode tile,
+    two fill the 32-row tile, three (48 rows) go to the prefill kernel."""
+    need_gpu()
+    b = W.build_batch([40, 900, 3001], [nq] * 3, 64, 4, seed=32 + nq)
+    _run_and_check(b)
+
+
+def test_decode_many_sequences():
+    """300 sequences: the device-side plan scans run over several 64-wide
+    chunks of sequences, and contexts of 1..600 tokens leave many segments
+    whole inside one workgroup and others split."""
+    need_gpu()
+    rng = np.random.default_rng(33)
+    b = W.build_batch(rng.integers(1, 601, 300), [1] * 300, 8, 1, seed=33)
+    _run_and_check(b)
+
+
+def test_prefill_mha_several_row_tiles():
+    """G = 1 (16/16 heads): a 600-token prefill spans three 256-row tiles;
+    lengths off the 16-token grid."""
+    need_gpu()
+    b = W.build_batch([600, 257], [600, 250], 16, 16, seed=34)
+    _run_and_check(b)
+
+
 def test_inline_causal_chunked_prefill():
     """tests/test_inline_causal.py: 8/2 heads, seq 512/384, chunks 256/128."""
     need_gpu()
@@ -338,3 +374,27 @@ def test_mixed_many_chunks():
     sl = [q + int(c) for q, c in zip(ql, rng.integers(0, 3001, len(ql)))]
     b = W.build_batch(sl, ql, 12, 3, seed=22)
     _run_and_check(b)
+
+
+def test_forward_paged_returns_flat_fp32_and_logs(tmp_path, monkeypatch):
+    """gfx906_fa_paged.forward_paged with no ``out`` returns what the
+    reference's dispatcher returns, ``[num_tokens, Hq*D]`` fp32
+    (extension/gfx906_fa_paged.py:197-465), for a mixed decode + chunked
+    prefill batch; with GFX906_FA_FWD_DEBUG on, the call is logged before the
+    launch and OK after it."""
+    need_gpu()
+    import gfx906_fa_paged as P
+    monkeypatch.setattr(P, "_DBG", True)
+    monkeypatch.setattr(P, "_DBG_DIR", str(tmp_path))
+    announce("forward_paged flat fp32 + debug log")
+    b = W.build_batch([700, 33, 1500], [1, 33, 200], 8, 2, seed=21)
+    kp, vp = b.planes()
+    res = P.forward_paged(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t, b.max_query_len,
+                          b.max_seq_len, b.scale)
+    torch.cuda.synchronize()
+    assert res.dtype == torch.float32 and tuple(res.shape) == (b.num_tokens, b.Hq * b.D)
+    assert_close(res.view(b.num_tokens, b.Hq, b.D).cpu().numpy(), batch_oracle(b))
+    lines = (tmp_path / f"fwd-{os.getpid()}.log").read_text().splitlines()
+    assert len(lines) == 2
+    assert "forward_paged VARLEN: num_tokens=234 Hq=8 Hkv=2" in lines[0]
+    assert "forward_paged OK: out=(234, 8, 128)" in lines[1]
