@@ -743,13 +743,20 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
-constexpr int PF_WAVES = 8;
+#ifndef GFA_PF_WAVES
+#define GFA_PF_WAVES 8
+#endif
+constexpr int PF_WAVES = GFA_PF_WAVES;        // 8 (2 waves per SIMD) or 4 (1 wave per SIMD)
 constexpr int PF_ROWS = 32 * PF_WAVES;
 #ifndef GFA_PF_TK
 #define GFA_PF_TK 64
 #endif
 constexpr int PF_TK = GFA_PF_TK;              // keys per LDS tile: 64 or 128
 constexpr int PF_NSP = PF_TK / 16;            // sub-pages per tile
+// a wave fetches and dequantizes both halves of one sub-page per tile
+// (PF_NSP == PF_WAVES) or one half (2 * PF_NSP == PF_WAVES)
+constexpr bool PF_BOTH = PF_NSP == PF_WAVES;
+static_assert(PF_BOTH || 2 * PF_NSP == PF_WAVES, "tile / wave split");
 constexpr int PF_NST = PF_TK / 32;            // 32-key S subtiles per tile
 constexpr int PF_KPITCH = 272;
 constexpr int PF_VPITCH = 2 * PF_TK + 16;
@@ -861,7 +868,7 @@ __device__ __forceinline__ void pf_dequant_v(const PfRaw &r, uint8_t *vst, int s
 
 template <int QDT, int ODT, bool VF16, bool MASK>
 __global__ __launch_bounds__(64 * PF_WAVES)
-__attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p) {
+__attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefill_kernel(AttnParams p) {
     // two LDS stages of K^ and of V^, each a distinct object: the compiler
     // can then prove that the dequant stores (one stage) and the MFMA operand
     // reads (the other) are independent and interleave them
@@ -927,10 +934,10 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
     const int bs = p.block_size;
     const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
-    // 64-key tiles: wave w takes half w/4 of sub-page w%4; 128-key tiles:
-    // wave w takes both halves of sub-page w
-    const int wsp = PF_NSP == 4 ? (w & 3) : w;
-    const int hf = PF_NSP == 4 ? (w >> 2) : 0;
+    // 8 waves over 64-key tiles: wave w takes half w/4 of sub-page w%4;
+    // otherwise wave w takes both halves of sub-page w
+    const int wsp = PF_BOTH ? w : w % PF_NSP;
+    const int hf = PF_BOTH ? 0 : w / PF_NSP;
     auto sp_of = [&](int kt) { return min(PF_NSP * kt + wsp, last_sp); };
     auto load_pg = [&](int c) -> int {
         const int kt = 64 * c + lane;
@@ -946,7 +953,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
     // the K/V fetches of the previous step included.
     auto ready = [](int &v) { asm volatile("" : "+v"(v)); };
     struct PfRawT {
-        PfRaw h[PF_NSP == 8 ? 2 : 1];
+        PfRaw h[PF_BOTH ? 2 : 1];
     };
     auto fetch = [&](PfRawT &rw, int kt) {
         const int rel = kt - cbase;  // 0..127, uniform
@@ -957,16 +964,16 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnParams p
         const uint8_t *kb = kplane + page * p.cbs + spi * SUBPAGE_BYTES;
         const uint8_t *vb = vplane + page * p.vcbs + spi * VSUB;
         pf_fetch<VF16>(rw.h[0], kb, vb, lane, hf);
-        if constexpr (PF_NSP == 8) pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
+        if constexpr (PF_BOTH) pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
     };
     auto dequant_k = [&](const PfRawT &rw, uint8_t *kst) {
         pf_dequant_k(rw.h[0], kst, wsp, lane, hf);
-        if constexpr (PF_NSP == 8) pf_dequant_k(rw.h[1], kst, wsp, lane, 1);
+        if constexpr (PF_BOTH) pf_dequant_k(rw.h[1], kst, wsp, lane, 1);
     };
     auto dequant_v = [&](const PfRawT &rw, uint8_t *vst, auto tail) {
         constexpr bool T = decltype(tail)::value;
         pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, hf);
-        if constexpr (PF_NSP == 8) pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
+        if constexpr (PF_BOTH) pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
     };
 
     float16v_t o[4];
