@@ -22,7 +22,9 @@ Also reported on the same JSON line:
                   attention rate against it.
   prefill       - cfg3 (32K causal prefill, bf16, 48/8): attention TFLOP/s
                   (4*D*Hq*sum of visible keys) vs 2.5 PFLOP/s dense fp16/bf16
-                  MFMA peak, the K/V quantize-write GB/s, and the fused
+                  MFMA peak, ``mfma_busy`` (the MFMA-busy fraction of the
+                  kernel's SIMD-cycles from the committed rocprofv3 PMC
+                  summary), the K/V quantize-write GB/s, and the fused
                   rotary + K/V write GB/s (vs 8 TB/s) over the same tokens.
   cpu_baseline  - the reference's PyTorch CPU path (paged gather + dequantize
                   + fp32 SDPA, oracle/cpu_baseline.py) on whole cfg2
@@ -65,16 +67,22 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def _traffic(kernel_tag: str):
-    """HBM bytes per launch from a committed rocprofv3 PMC summary, or None."""
-    p = os.path.join(ROOT, "profiles", f"{kernel_tag}_traffic.json")
+def _profile_value(name: str, key: str):
+    """A figure from a committed rocprofv3 PMC summary (profiles/<name>.json),
+    or None."""
+    p = os.path.join(ROOT, "profiles", f"{name}.json")
     if os.path.exists(p):
         try:
             with open(p) as f:
-                return json.load(f).get("hbm_bytes_per_launch")
+                return json.load(f).get(key)
         except (OSError, ValueError):
             return None
     return None
+
+
+def _traffic(kernel_tag: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, or None."""
+    return _profile_value(f"{kernel_tag}_traffic", "hbm_bytes_per_launch")
 
 
 def timed(fn, steps: int, warmup: int):
@@ -147,7 +155,8 @@ def other_workload(args, dev) -> dict:
         res.update({"value": round(tfs, 2), "unit": "TFLOP/s"})
         res["roofline"] = {"bound": "mfma", "kernel": "attn_prefill_kernel", "achieved": round(tfs, 2),
                            "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_PEAK_TFLOPS, 4),
-                           "traffic": None, "avg_us": round(ms * 1e3, 2)}
+                           "traffic": None, "avg_us": round(ms * 1e3, 2),
+                           "mfma_busy": _profile_value("attn_prefill_cfg3_mfma", "mfma_busy_frac")}
     else:  # cfg4: both bounds; the parts timed as batches of their own
         npf = int((b.q_lens > 1).sum())
         pf, dc = W.sub_batch(b, 0, npf), W.sub_batch(b, npf, b.num_seqs)
@@ -310,6 +319,7 @@ def main() -> int:
             "attn_ms": round(ms_p, 4), "tflops": round(fl / (ms_p * 1e-3) / 1e12, 2),
             "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
             "frac": round(fl / (ms_p * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4), "flop": fl,
+            "mfma_busy": _profile_value("attn_prefill_cfg3_mfma", "mfma_busy_frac"),
             "kv_write_ms": round(ms_w, 4), "kv_write_gbs": round(wbytes / (ms_w * 1e-3) / 1e9, 1),
             "rope_kv_write_ms": round(ms_r, 4), "rope_kv_write_bytes": rbytes,
             "rope_kv_write_gbs": round(rbytes / (ms_r * 1e-3) / 1e9, 1),
