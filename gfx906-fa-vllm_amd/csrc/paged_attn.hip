@@ -402,7 +402,10 @@ __device__ __forceinline__ void write_new_token(const AttnParams &p, int h, int6
 }
 
 constexpr int DEC_NW = 4;          // waves per decode workgroup
-constexpr int DEC_MIN_UNITS = 16;  // sub-pages per decode workgroup, at least
+#ifndef GFA_DEC_MIN_UNITS
+#define GFA_DEC_MIN_UNITS 16
+#endif
+constexpr int DEC_MIN_UNITS = GFA_DEC_MIN_UNITS;  // sub-pages per decode workgroup, at least
 
 #ifndef GFA_DEC_DEPTH2
 #define GFA_DEC_DEPTH2 2
@@ -449,17 +452,24 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
            (uint32_t)__builtin_amdgcn_readfirstlane((int)(v & 0xFFFFFFFF));
 }
 
-// Total decode units U and the number of participating workgroups (every
-// range non-empty and at least DEC_MIN_UNITS long).  Wave-level, uniform.
+// Total decode units U and the number of participating workgroups: at least
+// DEC_MIN_UNITS units per range, or one workgroup per segment where segments
+// are shorter than that (each piece a workgroup streams costs a Q load and a
+// cross-wave merge, so many short pieces in one range serialize), and at
+// most the resident workgroups.  Every range is non-empty: each counted
+// segment holds at least one unit.  Wave-level, uniform.
 __device__ __forceinline__ void dec_total(const AttnParams &p, int lane, int64_t &U, int &nwg) {
     int64_t tot = 0;
+    int nseg = 0;
     for (int base = 0; base < p.num_seqs; base += 64) {
         const int si = base + lane;
         const int n = si < p.num_seqs ? seg_info(p, si).nsub : 0;
         tot += __shfl(wave_incl_scan(n, lane), 63);
+        nseg += __builtin_popcountll(__ballot(n > 0));
     }
     U = uniform64(tot * p.Hkv);
-    nwg = (int)max((int64_t)1, min((int64_t)p.nwg, U / DEC_MIN_UNITS));
+    const int64_t want = max(U / DEC_MIN_UNITS, (int64_t)nseg * p.Hkv);
+    nwg = (int)max((int64_t)1, min((int64_t)p.nwg, want));
 }
 
 __device__ __forceinline__ int64_t range_start(int64_t U, int k, int n) { return U * k / n; }
