@@ -26,6 +26,11 @@ Also reported on the same JSON line:
                   kernel's SIMD-cycles from the committed rocprofv3 PMC
                   summary), the K/V quantize-write GB/s, and the fused
                   rotary + K/V write GB/s (vs 8 TB/s) over the same tokens.
+  next_rows     - graph capture: the cfg2 step and a 32 x 32-token decode
+                  batch per call, eager vs replayed from a HIP graph; the
+                  output epilogue: the reference's fp32 BSHD -> BHSD ->
+                  model-dtype copies timed at cfg3's output size (here the
+                  kernels write the model dtype in place).
   cpu_baseline  - the reference's PyTorch CPU path (paged gather + dequantize
                   + fp32 SDPA, oracle/cpu_baseline.py) on whole cfg2
                   sequences, repeated for a ~10 s budget, same GB/s accounting.
@@ -101,6 +106,75 @@ def timed(fn, steps: int, warmup: int):
     e.record(stream)
     torch.cuda.synchronize()
     return s.elapsed_time(e) / steps
+
+
+def graph_timed(fn, calls: int = 20, replays: int = 10):
+    """Average ms of fn() replayed from a HIP graph that captures `calls`
+    back-to-back calls (the host launch cost of the eager loop removed)."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / (replays * calls)
+
+
+def graph_replay_times(args, step, dev) -> dict:
+    """Per-call time of the cfg2 step and of a small decode batch (32
+    sequences of 32 tokens, 48/8), eager vs replayed from a HIP graph."""
+    import torch
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+    sb = W.build_batch([32] * 32, [1] * 32, 48, 8, seed=5, device=dev)
+    skp, svp = sb.planes()
+    sout = torch.empty((sb.num_tokens, sb.Hq, sb.D), dtype=torch.float16, device=dev)
+    sws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(
+        sb.num_seqs, sb.num_tokens, sb.Hq, sb.Hkv, sb.max_query_len, sb.max_seq_len), dev)
+
+    def small():
+        gfx906_fa.paged_attention(sb.query, skp, svp, sb.block_table, sb.seq_lens_t, sb.qsl_t,
+                                  sb.max_query_len, sb.max_seq_len, sb.scale, out=sout, workspace=sws)
+
+    return {
+        "cfg2_step_us": {"eager": round(timed(step, args.steps, args.warmup) * 1e3, 2),
+                         "graph": round(graph_timed(step) * 1e3, 2)},
+        "small_decode_us": {"workload": "32 seqs x 32 tokens, 48/8",
+                            "eager": round(timed(small, 200, 50) * 1e3, 2),
+                            "graph": round(graph_timed(small) * 1e3, 2)},
+    }
+
+
+def output_epilogue_ms(dev) -> dict:
+    """The reference's output epilogue - fp32 BSHD result transposed to BHSD,
+    then copied into the model-dtype output (extension/gfx906_fa.cpp:264,
+    extension/gfx906_fa_backend.py:527-528) - timed at cfg3's output size.
+    The kernels here write the model dtype in place: no epilogue."""
+    import torch
+    T3, H3 = 32768, 48
+    o32 = torch.empty((1, T3, H3, 128), dtype=torch.float32, device=dev)
+    o16 = torch.empty((T3, H3 * 128), dtype=torch.bfloat16, device=dev)
+
+    def ref_epilogue():
+        bhsd = o32.transpose(1, 2).contiguous()
+        o16.copy_(bhsd.transpose(1, 2).reshape(T3, H3 * 128))
+
+    o32.normal_()
+    ms = timed(ref_epilogue, 10, 3)
+    del o32, o16
+    torch.cuda.empty_cache()
+    return {"workload": "cfg3 output, 32768 x 48 x 128", "reference_epilogue_ms": round(ms, 4), "here_ms": 0.0}
 
 
 def _attn_fn(b, out, ws):
@@ -280,6 +354,11 @@ def main() -> int:
         },
     }
 
+    # ---------------- the rows after the hot path -------------------------
+    # graph capture (not in the counter calibration runs, which profile the
+    # eager kernels only)
+    graph = None if args.calib_copy_mib else graph_replay_times(args, step, dev)
+
     # ---------------- cfg3 prefill (secondary) ------------------------------
     if not args.no_prefill:
         del b, out, ws
@@ -327,6 +406,10 @@ def main() -> int:
         }
         del p, pout
         torch.cuda.empty_cache()
+
+    if graph is not None:
+        res["next_rows"] = {"graph_replay": graph,
+                            "output_epilogue": output_epilogue_ms(dev)}
 
     if args.calib_copy_mib:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE
