@@ -53,8 +53,15 @@ def test_validation_errors_without_gpu():
     # planar write: head size must be 128
     assert L.gfx906_fa_amd_cache_write_kv(None, None, 1, None, None, None, 1, 1, 64, 16,
                                           0, 0, 0, 0, 0, 0, None) == 1
-    # empty work is a no-op success
+    # empty work is a no-op success (returns before any HIP call)
     assert L.gfx906_fa_amd_quantize_q8_0(None, 1, None, 0, 128, None) == 0
+    assert L.gfx906_fa_amd_cache_write_kv(None, None, 1, None, None, None, 0, 8, 128, 16,
+                                          0, 0, 0, 0, 0, 0, None) == 0
+    assert L.gfx906_fa_amd_paged_attention(None, 1, 0, 0, None, None, 0, 0, None, 0, None, None,
+                                           None, 1, 0, 0, 48, 8, 128, 16, 1, 16, 0.1, None, 1, 0, 0,
+                                           None, 0, None) == 0
+    assert L.gfx906_fa_amd_gather_planar(None, None, None, None, None, None, 0, 8, 32, 128, 16, 4,
+                                         0, 0, None) == 0
     # fused rotary + write: rot_dim 72 is not a multiple of 16 (neox); fp32 rows;
     # a valid configuration with no tokens is a no-op
     rope = L.gfx906_fa_amd_rope_cache_write_kv
