@@ -25,7 +25,8 @@ Also reported on the same JSON line:
                   MFMA peak, ``mfma_busy`` (the MFMA-busy fraction of the
                   kernel's SIMD-cycles from the committed rocprofv3 PMC
                   summary), the K/V quantize-write GB/s, and the fused
-                  rotary + K/V write GB/s (vs 8 TB/s) over the same tokens.
+                  rotary + K/V write GB/s (vs 8 TB/s) over the same tokens,
+                  for the bf16 model and again for an fp16 one.
   next_rows     - graph capture: the cfg2 step and a 32 x 32-token decode
                   batch per call, eager vs replayed from a HIP graph; the
                   output epilogue: the reference's fp32 BSHD -> BHSD ->
@@ -390,6 +391,15 @@ def main() -> int:
         ms_p = timed(pattn, psteps, 2)
         ms_w = timed(pwrite, psteps, 2)
         ms_r = timed(prope, psteps, 2)
+        # the same write for an fp16 model (its own kernel instantiation)
+        q16, k16, v16 = p.query.half(), p.key.half(), p.value.half()
+        cs16 = W.rope_cos_sin_cache(T3, p.D, torch.float16, dev)
+
+        def prope16():
+            gfx906_fa.rope_and_cache_q8_kv(pos3, q16, k16, v16, cs16, True, p.slot_mapping, pk, pv)
+
+        ms_r16 = timed(prope16, psteps, 2)
+        del q16, k16, v16
         rbytes = W.rope_write_bytes(T3, p.Hq, p.Hkv, p.D)
         fl = p.flops()
         wbytes = p.key.numel() * 2 * 2 + p.key.shape[0] * p.Hkv * 2 * 136 + p.key.shape[0] * 8
@@ -403,6 +413,8 @@ def main() -> int:
             "rope_kv_write_ms": round(ms_r, 4), "rope_kv_write_bytes": rbytes,
             "rope_kv_write_gbs": round(rbytes / (ms_r * 1e-3) / 1e9, 1),
             "rope_kv_write_frac": round(rbytes / (ms_r * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "rope_kv_write_f16_ms": round(ms_r16, 4),
+            "rope_kv_write_f16_gbs": round(rbytes / (ms_r16 * 1e-3) / 1e9, 1),
         }
         del p, pout
         torch.cuda.empty_cache()

@@ -215,8 +215,11 @@ constexpr int ROPE_ITERS = GFA_ROPE_ITERS;  // row quads per wave: 8 x 4 = 32 ro
 // Wave (token t, chunk c) takes the token's rows 32c .. 32c+31 of the list
 // [Hq query heads, Hkv key heads]: iteration it, lane row g -> row
 // 32c + 4it + g (32 rows per wave measured 4 % faster than 16 and 56).
+// At least 4 waves per SIMD: left to itself the compiler gives the fp16
+// instantiations 234-238 VGPRs (one wave per SIMD, half the bf16 rate); at
+// this bound both dtypes fit 104-114 with no spills.
 template <int DT, int CSDT, bool NEOX>
-__global__ __launch_bounds__(256) void q8_rope_cache_write_kernel(RopeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q8_rope_cache_write_kernel(RopeArgs a) {
     const int64_t wave = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int i = lane & 15, g = lane >> 4;
