@@ -1,7 +1,7 @@
 """Benchmark of the Q8_0 paged-attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 200] [--no-cpu] [--no-prefill]
-    python bench.py --workload {cfg3,cfg4,cfg5,cfg5-48}   (one other configuration)
+    python bench.py --workload {cfg3,cfg4,cfg5,cfg5-48,cfg5-k6}   (one other configuration)
 
 Headline (``value``): batched decode, cfg2 of the benchmark definition - 32 sequences with
 contexts U[2048, 16384], 48 query / 8 KV heads, head_dim 128, fp16 Q, Q8_0
@@ -41,7 +41,8 @@ definition instead (the line's roofline is that workload's dominant kernel):
   cfg3     32K causal prefill (MFMA-bound: TFLOP/s)
   cfg4     mixed chunked prefill + decode; the prefill chunks and the decode
            sequences are also timed as batches of their own (``parts``)
-  cfg5     speculative verify, 6/1 heads (HBM-bound: GB/s); cfg5-48: 48/8 heads
+  cfg5     speculative verify, 6/1 heads (HBM-bound: GB/s); cfg5-48: 48/8 heads;
+           cfg5-k6: 6 verify tokens (the reference's n-gram k=5), 36 rows
 """
 from __future__ import annotations
 
@@ -196,7 +197,8 @@ def other_workload(args, dev) -> dict:
     import gfx906_fa
     import gfx906_fa_workloads as W
 
-    name = "cfg5" if args.workload.startswith("cfg5") else args.workload
+    name = {"cfg5-48": "cfg5", "cfg5-k6": "cfg5k6"}.get(args.workload, args.workload)
+    verify = name in ("cfg5", "cfg5k6")
     heads = (48, 8) if args.workload == "cfg5-48" else None
     b = W.build_cfg(name, device=dev, heads=heads)
     odt = torch.bfloat16 if b.dtype == "bf16" else torch.float16
@@ -208,9 +210,9 @@ def other_workload(args, dev) -> dict:
         return gfx906_fa.new_workspace(gfx906_fa.workspace_size(
             bb.num_seqs, bb.num_tokens, bb.Hq, bb.Hkv, bb.max_query_len, bb.max_seq_len), dev)
 
-    steps = args.steps if name == "cfg5" else max(3, min(10, args.steps // 5))
+    steps = args.steps if verify else max(3, min(10, args.steps // 5))
     # warm-up: the given steps, at least ~20 ms of work for the short passes
-    ms = timed(_attn_fn(b, new_out(b), new_ws(b)), steps, max(2, args.warmup if name == "cfg5" else 2))
+    ms = timed(_attn_fn(b, new_out(b), new_ws(b)), steps, max(2, args.warmup if verify else 2))
     fl, hb = b.flops(), b.hbm_bytes(out_bytes_per_elem=2)
     gbs, tfs = hb / (ms * 1e-3) / 1e9, fl / (ms * 1e-3) / 1e12
     res = {
@@ -221,7 +223,7 @@ def other_workload(args, dev) -> dict:
                    "num_tokens": b.num_tokens, "heads": f"{b.Hq}/{b.Hkv}", "total_context": int(b.seq_lens.sum()),
                    "algorithmic_bytes": hb, "flop": fl, "parallelism": "single GPU"},
     }
-    if name == "cfg5":
+    if verify:
         res.update({"value": round(gbs, 1), "unit": "GB/s"})
         res["roofline"] = {"bound": "hbm", "kernel": "attn_decode_kernel+attn_combine_kernel",
                            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -266,7 +268,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (rocprof counter calibration)")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5", "cfg5-48"])
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5", "cfg5-48", "cfg5-k6"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

@@ -74,6 +74,7 @@ struct AttnParams {
     int num_seqs, nwg;    // nwg: decode workgroups (the grid)
     int dec_rows_lo;      // a decode launch takes sequences with dec_rows_lo < n_q*G
     int dec_rows_max;     //   <= dec_rows_max; the prefill kernel takes n_q*G > dec_rows_max
+                          //   (in a decode launch also the rows of its partial slots)
     // prefill work list (heaviest first) built by prefill_plan_kernel: item i
     // is row tile pf_rt[i] of sequence pf_seq[i], *pf_count items.
     // nullptr: the prefill grid is (row tiles * Hkv, num_seqs) instead.
@@ -402,6 +403,7 @@ __device__ __forceinline__ void write_new_token(const AttnParams &p, int h, int6
 }
 
 constexpr int DEC_NW = 4;          // waves per decode workgroup
+constexpr int DEC_CHUNK_ROWS = 64; // rows the two-row-group launch takes, in 32-row chunks
 #ifndef GFA_DEC_MIN_UNITS
 #define GFA_DEC_MIN_UNITS 16
 #endif
@@ -476,7 +478,10 @@ __device__ __forceinline__ int64_t range_start(int64_t U, int k, int n) { return
 // the workgroup whose range holds unit u
 __device__ __forceinline__ int range_of(int64_t U, int64_t u, int n) { return (int)(((u + 1) * n - 1) / U); }
 
-template <int NRG, int QDT, int ODT>
+// CHUNK: sequences may have more rows than one tile (up to dec_rows_max):
+// each piece is streamed once per R-row chunk.  A separate instantiation, so
+// the launches that never need it keep their register allocation.
+template <int NRG, int QDT, int ODT, bool CHUNK = false>
 __global__ __launch_bounds__(64 * DEC_NW)
 __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void attn_decode_kernel(AttnParams p) {
     constexpr int R = 16 * NRG;  // rows per slot
@@ -579,9 +584,13 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         const int b = (int)min((int64_t)si.nsub, a + (u1 - u));
         const int nrows = si.nq * p.G;
 
+        // CHUNK: rows beyond one tile (up to 64: a verify step of 6 tokens at
+        // 6 q-heads per kv-head is 36 rows) are taken R at a time, each chunk
+        // streaming the piece's keys again; otherwise one pass
+        auto rows_pass = [&](int rc) {
         half8_t qf[NRG][4];
         int lim[NRG];
-        load_rows<NRG, QDT>(p, h, si.q0, nrows, 0, si.sl, si.qa, i16, g, qf, lim);
+        load_rows<NRG, QDT>(p, h, si.q0, nrows, rc, si.sl, si.qa, i16, g, qf, lim);
         WaveAcc<NRG> acc;
         acc_init(acc);
         stream_range<NRG, GFA_DEC_NT != 0, DecCfg<NRG>::depth>(acc, p, s, h, 16 * a,
@@ -603,19 +612,21 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         __syncthreads();
         const bool whole = a == 0 && b == si.nsub;
         const int slot = 2 * w + (first ? 0 : 1);
-        for (int it = threadIdx.x; it < nrows * 32; it += 64 * DEC_NW) {
-            const int r = it >> 5, d0 = (it & 31) * 4;
+        const int rows_c = CHUNK ? min(R, nrows - rc) : nrows;
+        for (int it = threadIdx.x; it < rows_c * 32; it += 64 * DEC_NW) {
+            const int rl = it >> 5, d0 = (it & 31) * 4;
+            const int r = rc + rl;
             float mx = -INFINITY;
 #pragma unroll
-            for (int k = 0; k < DEC_NW; ++k) mx = fmaxf(mx, sm_m[k][r]);
+            for (int k = 0; k < DEC_NW; ++k) mx = fmaxf(mx, sm_m[k][rl]);
             const float ms = mx == -INFINITY ? 0.0f : mx;
             float l = 0.f;
             float4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k < DEC_NW; ++k) {
-                const float wk = __builtin_amdgcn_exp2f(sm_m[k][r] - ms);
-                l = fmaf(sm_l[k][r], wk, l);
-                o += *reinterpret_cast<const float4_t *>(&sm_o[k][r][d0]) * wk;
+                const float wk = __builtin_amdgcn_exp2f(sm_m[k][rl] - ms);
+                l = fmaf(sm_l[k][rl], wk, l);
+                o += *reinterpret_cast<const float4_t *>(&sm_o[k][rl][d0]) * wk;
             }
             if (whole) {
                 const int j = r / p.G;
@@ -625,7 +636,7 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
 #pragma unroll
                 for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
             } else {
-                const int64_t row = (int64_t)slot * R + r;
+                const int64_t row = (int64_t)slot * (CHUNK ? p.dec_rows_max : R) + r;
                 *reinterpret_cast<float4_t *>(p.ws_o + row * 128 + d0) = o;
                 if (d0 == 0) {
                     p.ws_ml[2 * row] = mx;
@@ -633,7 +644,13 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
                 }
             }
         }
-        __syncthreads();  // LDS reused by the next piece
+        __syncthreads();  // LDS reused by the next row chunk / piece
+        };
+        if constexpr (CHUNK) {
+            for (int rc = 0; rc < nrows; rc += R) rows_pass(rc);
+        } else {
+            rows_pass(0);
+        }
         u += b - a;
         first = false;
         if (u < u1 && b == si.nsub && h == Hkv - 1) {  // next sequence with decode work
@@ -681,7 +698,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     float4_t o = {0.f, 0.f, 0.f, 0.f};
     for (int k = wf + sub; k <= wl; k += 8) {
         const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
-        const int64_t row = (int64_t)sk * R + r;
+        const int64_t row = (int64_t)sk * p.dec_rows_max + r;
         const float mk = p.ws_ml[2 * row], lk = p.ws_ml[2 * row + 1];
         const float4_t ok = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
         const float mn = fmaxf(m, mk);
@@ -1294,7 +1311,9 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
 // Decode work is split by packed rows per sequence into classes, each with
 // its own stream-K plan, workspace region and combine: n_q*G <= 16 runs the
 // one-row-group kernel (three waves per SIMD), 16 < n_q*G <= 32 the
-// two-row-group kernel (speculative verify).  A batch whose sequences all have
+// two-row-group kernel (speculative verify), and up to 64 rows its chunked
+// instantiation (32 rows per pass, 64-row partial slots; only when the
+// batch's max_query_len * G exceeds 32).  A batch whose sequences all have
 // max_query_len tokens (num_tokens == num_seqs * max_query_len) needs at
 // most one class, and a uniform prefill batch none; a class launched alone
 // takes every row count up to its bound.  Sequences above the largest bound
@@ -1343,13 +1362,15 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
         c.rows_hi = hi;
         c.nwg = device_cus() * 4 * (nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe) / DEC_NW;
     };
+    // the two-row-group class takes up to DEC_CHUNK_ROWS rows in 32-row chunks
+    const int hi2 = max_rows <= 32 ? 32 : DEC_CHUNK_ROWS;
     if (max_rows <= 16) {
         add(1, 0, 16);
     } else if (uniform) {
-        if (max_rows <= 32) add(2, 0, 32);
+        if (max_rows <= DEC_CHUNK_ROWS) add(2, 0, hi2);
     } else {
         if (G <= 16) add(1, 0, 16);
-        if (G <= 32) add(2, pl.ndc ? 16 : 0, 32);
+        if (G <= DEC_CHUNK_ROWS) add(2, pl.ndc ? 16 : 0, hi2);
     }
     pl.dec_rows_max = pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0;
     pl.need_prefill = max_rows > pl.dec_rows_max;
@@ -1360,7 +1381,7 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     size_t off = 0;
     for (int k = 0; k < pl.ndc; ++k) {
         DecClass &c = pl.dc[k];
-        const size_t rc = (size_t)16 * c.nrg;
+        const size_t rc = (size_t)c.rows_hi;  // rows per partial slot
         c.off_hdr = off;
         c.off_pre = off + 256;
         c.off_ml = c.off_pre + align256((size_t)num_seqs * sizeof(int));
@@ -1396,7 +1417,8 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
             attn_decode_kernel<1, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
             attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
         } else {
-            attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
+            if (c.rows_hi > 32) attn_decode_kernel<2, QDT, ODT, true><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
+            else attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
             attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
         }
     }

@@ -198,6 +198,7 @@ CONFIGS = {
     "cfg3": "1 seq x 32768 causal prefill, 48/8 heads, bf16",
     "cfg4": "4 chunks x 2048 (prior 0/16K/32K/64K) + 60 decodes ctx logU[1K,128K], 48/8, fp16",
     "cfg5": "8 seqs x 131072 cached + 5 verify tokens, 6/1 heads (and 48/8), fp16",
+    "cfg5k6": "8 seqs x 131072 cached + 6 verify tokens (n-gram k=5), 6/1 heads, fp16",
 }
 
 
@@ -217,9 +218,12 @@ def cfg_shape(name: str, seed: int = 0, heads=None):
         ql = [2048] * 4
         dec = np.exp(rng.uniform(math.log(1024), math.log(131072), size=60)).astype(np.int64)
         return sl + dec.tolist(), ql + [1] * 60, 48, 8, "f16"
-    if name == "cfg5":
+    if name in ("cfg5", "cfg5k6"):
+        # cfg5k6: the verify step of the reference's n-gram serving setting,
+        # num_speculative_tokens = 5 plus the bonus token (36 rows at 6/1)
         hq, hkv = heads or (6, 1)
-        return [131072 + 5] * 8, [5] * 8, hq, hkv, "f16"
+        nq = 5 if name == "cfg5" else 6
+        return [131072 + nq] * 8, [nq] * 8, hq, hkv, "f16"
     raise KeyError(name)
 
 

@@ -195,7 +195,7 @@ hipError_t gfx906_fa_amd_rope_cache_write_kv(
  *     of at least gfx906_fa_amd_paged_attention_workspace_size(...) bytes,
  *     256-byte aligned (no initial contents needed: each call writes what it
  *     reads).  Calls sharing one workspace must be ordered (same stream).
- *     Decode-shaped sequences (n_q*Hq/Hkv <= 32 rows) are split stream-K
+ *     Decode-shaped sequences (n_q*Hq/Hkv <= 64 rows) are split stream-K
  *     style: the device's resident workgroups each stream an equal,
  *     contiguous share of all their 16-token KV sub-pages; segments cut
  *     between workgroups leave partial (m, l, O) in the workspace and a
@@ -219,7 +219,7 @@ hipError_t gfx906_fa_amd_paged_attention(
 /* (5b) (4) followed by (5) in one call: key / value [num_tokens, Hkv, D] (the
  *      query dtype, element strides) are quantized to Q8_0 and written at
  *      slot_mapping[t] (< 0 = skip) before attention reads the cache.  When
- *      every sequence is decode-shaped (n_q*Hq/Hkv <= 32 rows) and
+ *      every sequence is decode-shaped (n_q*Hq/Hkv <= 64 rows) and
  *      q_abs_offset is NULL, the new tokens are the last n_q positions of
  *      their sequences and the decode kernel itself quantizes each one in the
  *      wave that streams its sub-page, uses those bytes for attention and

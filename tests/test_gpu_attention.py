@@ -149,9 +149,29 @@ def test_spec_verify(heads):
 
 
 def test_verify_more_rows_than_decode_tile():
-    """n_q*G = 48 > 32 rows goes to the prefill kernel."""
+    """n_q*G = 48 > 32 rows: the two-row-group launch takes them in two
+    32-row chunks."""
     need_gpu()
     b = W.build_batch([900, 40], [8, 8], 6, 1, seed=8)
+    _run_and_check(b)
+
+
+@pytest.mark.parametrize("case", [
+    ("6 tokens 6/1", [3000, 6, 1200, 17, 20000], [6] * 5, 6, 1, 16),      # 36 rows
+    ("7 tokens 6/1", [5000, 300, 64], [7] * 3, 6, 1, 16),                 # 42 rows
+    ("8 tokens 8/1", [2500, 9, 4100], [8] * 3, 8, 1, 16),                 # 64 rows
+    ("64/1 heads", [700, 33, 3000], [1] * 3, 64, 1, 16),                  # G = 64: 64 rows
+    ("mixed 5/6 tokens", [3000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # both decode classes
+    ("6 tokens 48/8 bs64", [2000, 6000, 333], [6] * 3, 48, 8, 64),
+])
+def test_verify_rows_33_to_64(case):
+    """Speculative verify with num_speculative_tokens = 5 (6 query tokens, the
+    reference's n-gram setting, scripts/start_vllm_fa_ngram.sh:35-39) packs
+    36 rows per kv-head at 6 q-heads: the decode kernel takes up to 64 rows in
+    32-row chunks instead of sending them to the prefill kernel."""
+    need_gpu()
+    name, sl, ql, hq, hkv, bs = case
+    b = W.build_batch(sl, ql, hq, hkv, block_size=bs, seed=80 + len(name))
     _run_and_check(b)
 
 

@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("fused", [False, True])
-@pytest.mark.parametrize("heads,q_len", [((48, 8), 1), ((6, 1), 5)])
+@pytest.mark.parametrize("heads,q_len", [((48, 8), 1), ((6, 1), 5), ((6, 1), 6)])
 def test_decode_step_graph_replay(heads, q_len, fused):
     """fused: the cache write folded into the attention call."""
     need_gpu()
