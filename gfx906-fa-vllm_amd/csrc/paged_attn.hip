@@ -76,10 +76,20 @@ struct AttnParams {
     int dec_rows_max;     //   <= dec_rows_max; the prefill kernel takes n_q*G > dec_rows_max
                           //   (in a decode launch also the rows of its partial slots)
     // prefill work list (heaviest first) built by prefill_plan_kernel: item i
-    // is row tile pf_rt[i] of sequence pf_seq[i], *pf_count items.
-    // nullptr: the prefill grid is (row tiles * Hkv, num_seqs) instead.
-    int *pf_seq, *pf_rt, *pf_count;
-    int pf_items_max;
+    // is key tiles [pf_kt0[i], pf_kt1[i]) of row tile pf_rt[i] of sequence
+    // pf_seq[i], *pf_count items; pf_slot[i] >= 0: a piece of a split row
+    // tile, whose partial (m, l, O) goes to partial slot pf_slot[i] (merged
+    // by attn_prefill_combine_kernel), else the piece is the whole row tile
+    // and writes the output.  nullptr: the prefill grid is
+    // (row tiles * Hkv, num_seqs) instead, with no split.
+    int *pf_seq, *pf_rt, *pf_kt0, *pf_kt1, *pf_slot, *pf_count;
+    int pf_items_max;   // row tiles, at most
+    int pf_grid_items;  // work-list capacity (the grid): row tiles + extra pieces
+    int pf_ncu;         // CUs the split targets
+    int pf_split_max;   // split row tiles, at most (also the extra pieces)
+    int pf_slots_max;   // partial slots per kv head
+    int *pf_split;      // split row tiles: (sequence, row tile, first slot, pieces) each
+    float *pf_ml, *pf_o;  // partials: [slot][Hkv][PF_ROWS] x (m, l) and x 128
     // Fused cache write of the step's new tokens (decode kernels only; nullptr:
     // none).  Row qsl[s] + j of new_k / new_v (the query dtype) holds the key /
     // value of position seq_lens[s] - n_q + j, written at slot new_slot[row].
@@ -905,12 +915,15 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     __shared__ __attribute__((aligned(16))) uint8_t ldsv1[PF_VBYTES];
     const int Hkv = p.Hkv;
     const int h = blockIdx.x % Hkv;
-    int s, rt;
+    int s, rt, kt0 = 0, kt1 = INT32_MAX, slot = -1;
     if (p.pf_seq) {  // the sorted work list (uniform)
         const int item = blockIdx.x / Hkv;
         if (item >= p.pf_count[0]) return;
         s = p.pf_seq[item];
         rt = p.pf_rt[item];
+        kt0 = p.pf_kt0[item];
+        kt1 = p.pf_kt1[item];
+        slot = p.pf_slot[item];
     } else {         // row tiles last-first within each sequence
         s = blockIdx.y;
         rt = (gridDim.x / Hkv) - 1 - (int)(blockIdx.x / Hkv);
@@ -928,7 +941,11 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
     const int jlast = (min(row0 + PF_ROWS, nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
-    const int ntk = (kv_end + PF_TK - 1) / PF_TK;
+    // key tiles [ktb, ktb + ntk) of the row tile's (kv_end + PF_TK - 1) / PF_TK;
+    // the loop below counts tiles from 0 and adds ktb where it needs a key index
+    const int ntk_all = (kv_end + PF_TK - 1) / PF_TK;
+    const int ktb = min(kt0, ntk_all);
+    const int ntk = min(kt1, ntk_all) - ktb;
 
     // this lane's query row, its causal bound and its Q^T fragments
     const int r = row0 + 32 * w + (lane & 31);
@@ -965,7 +982,8 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     // otherwise wave w takes both halves of sub-page w
     const int wsp = PF_BOTH ? w : w % PF_NSP;
     const int hf = PF_BOTH ? 0 : w / PF_NSP;
-    auto sp_of = [&](int kt) { return min(PF_NSP * kt + wsp, last_sp); };
+    const int spb = PF_NSP * ktb + wsp;
+    auto sp_of = [&](int kt) { return min(PF_NSP * kt + spb, last_sp); };
     auto load_pg = [&](int c) -> int {
         const int kt = 64 * c + lane;
         return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
@@ -1057,7 +1075,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
-        const int kbase_t = PF_TK * kt;
+        const int kbase_t = PF_TK * (kt + ktb);
         if constexpr (MASK) {  // S' += mask[s][j][key] (natural log units -> log2)
             const uint16_t *mrow = p.mask + (int64_t)s * p.mask_bs + (int64_t)j * p.mask_rs;
 #pragma unroll
@@ -1182,7 +1200,22 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     {
         auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
         const float l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-        if (rvalid) {
+        if (slot >= 0) {  // a piece of a split row tile: unnormalised O, m (log2), l
+            const int rl = 32 * w + (lane & 31);
+            const int64_t reg = (int64_t)slot * Hkv + h;
+            float *po = p.pf_o + (reg * PF_ROWS + rl) * 128 + 4 * hb;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                    *reinterpret_cast<float4_t *>(po + 32 * dt + 8 * q4) =
+                        float4_t{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+            if (hb == 0) {
+                float *pm = p.pf_ml + (reg * PF_ROWS + rl) * 2;
+                pm[0] = has_m ? m_use : -INFINITY;
+                pm[1] = l;
+            }
+        } else if (rvalid) {
             const float inv = l > 0.f ? 1.0f / l : 0.0f;
             const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + 4 * hb;
 #pragma unroll
@@ -1204,6 +1237,10 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
 constexpr int PL_THREADS = 1024;
 constexpr int PL_MAX_SEQS = 8192;  // larger batches keep the 2-D grid
 constexpr int PL_BUCKETS = 4096;   // key tiles per item, clamped (256K keys)
+#ifndef GFA_PF_SPLIT_MIN
+#define GFA_PF_SPLIT_MIN 16
+#endif
+constexpr int PF_SPLIT_MIN = GFA_PF_SPLIT_MIN;  // a split row tile's pieces: at least this many tiles
 
 // exclusive scan of v over the workgroup; *total receives the sum
 __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
@@ -1228,8 +1265,8 @@ __device__ __forceinline__ int pl_tiles(const AttnParams &p, int s) {
     return (nq > 0 && nrows > p.dec_rows_max) ? (nrows + PF_ROWS - 1) / PF_ROWS : 0;
 }
 
-// 64-key tiles row tile rt of sequence s attends (the prefill kernel's ntk)
-__device__ __forceinline__ int pl_weight(const AttnParams &p, int s, int rt) {
+// 64-key tiles row tile rt of sequence s attends (the prefill kernel's ntk_all)
+__device__ __forceinline__ int pl_ntk(const AttnParams &p, int s, int rt) {
     const int q0 = p.qsl[s];
     const int nq = p.qsl[s + 1] - q0;
     const int nrows = nq * p.G;
@@ -1237,13 +1274,34 @@ __device__ __forceinline__ int pl_weight(const AttnParams &p, int s, int rt) {
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
     const int jlast = (min(PF_ROWS * (rt + 1), nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
-    return min((kv_end + PF_TK - 1) / PF_TK, PL_BUCKETS - 1);
+    return (kv_end + PF_TK - 1) / PF_TK;
 }
+
+__device__ __forceinline__ int pl_bucket(int tiles) { return min(tiles, PL_BUCKETS - 1); }
+
+// sum of v over the workgroup (every thread receives it)
+__device__ __forceinline__ long long pl_block_sum(long long v, long long *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    __syncthreads();  // red[] of a previous call has been read
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    long long t = 0;
+#pragma unroll
+    for (int i = 0; i < PL_THREADS / 64; ++i) t += red[i];
+    return t;
+}
+
+// Pieces row tile of w key tiles is cut into when pieces hold at most tsplit
+// tiles; piece c of k covers tiles [c*w/k, (c+1)*w/k).
+__device__ __forceinline__ int pl_pieces(int w, int tsplit) { return w > tsplit ? (w + tsplit - 1) / tsplit : 1; }
 
 __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) {
     __shared__ int s_pre[PL_MAX_SEQS + 1];  // exclusive prefix of row tiles per sequence
     __shared__ int s_bk[PL_BUCKETS];        // bucket counts, then write cursors
     __shared__ int s_tmp[PL_THREADS];
+    __shared__ long long s_red[PL_THREADS / 64];
+    __shared__ int s_nsplit, s_nslot;
     const int B = p.num_seqs, tid = threadIdx.x;
     int carry = 0;
     for (int base = 0; base < B; base += PL_THREADS) {
@@ -1254,7 +1312,11 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         if (sq < B) s_pre[sq] = carry + ex;
         carry += tot;
     }
-    if (tid == 0) s_pre[B] = carry;
+    if (tid == 0) {
+        s_pre[B] = carry;
+        s_nsplit = 0;
+        s_nslot = 0;
+    }
     for (int b = tid; b < PL_BUCKETS; b += PL_THREADS) s_bk[b] = 0;
     __syncthreads();
     const int n = min(carry, p.pf_items_max);
@@ -1269,14 +1331,76 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         sq = lo;
         rt = i - s_pre[lo];
     };
+    // Split: a row tile longer than tsplit key tiles is cut into pieces of at
+    // most tsplit.  tsplit starts at one CU's share of the launch's key tiles
+    // (all row tiles x kv heads over pf_ncu; at least PF_SPLIT_MIN): split row
+    // tiles then number < pf_ncu / Hkv, their pieces < 2 pf_ncu / Hkv, and the
+    // extra work items < pf_ncu / Hkv; past the workspace's bounds
+    // (impossible by these sums) nothing is split.  With fewer row tiles than
+    // m = pf_ncu / Hkv, tsplit rises to the smallest value whose pieces fit
+    // one workgroup per CU (sum of pieces <= m): a few pieces over m would
+    // start a second round of workgroups and double the launch's time.
+    long long wsum = 0;
     for (int i = tid; i < n; i += PL_THREADS) {
         int sq, rt;
         locate(i, sq, rt);
-        atomicAdd(&s_bk[pl_weight(p, sq, rt)], 1);
+        wsum += pl_ntk(p, sq, rt);
+    }
+    const long long W = pl_block_sum(wsum, s_red);
+    long long tl = max((W * p.Hkv + p.pf_ncu - 1) / p.pf_ncu, (long long)PF_SPLIT_MIN);
+    const int m = p.pf_ncu / p.Hkv;
+    if (n < m && n <= PL_THREADS && p.pf_slots_max > 0) {
+        int wt = 0;  // thread t holds row tile t's key tiles
+        if (tid < n) {
+            int sq, rt;
+            locate(tid, sq, rt);
+            wt = pl_ntk(p, sq, rt);
+        }
+        // pieces(tsplit) is non-increasing; at hi it sums to <= W / hi + n <= m
+        long long lo = tl, hi = max(tl, (W + (m - n) - 1) / (m - n));
+        while (lo < hi) {
+            const long long mid = (lo + hi) >> 1;
+            const long long P = pl_block_sum(tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0, s_red);
+            if (P <= m) hi = mid;
+            else lo = mid + 1;
+        }
+        tl = lo;
+    }
+    int tsplit = p.pf_slots_max > 0 ? (int)min(tl, (long long)INT32_MAX) : INT32_MAX;
+    if (tsplit < INT32_MAX) {
+        long long ex = 0, sl = 0, ns = 0;
+        for (int i = tid; i < n; i += PL_THREADS) {
+            int sq, rt;
+            locate(i, sq, rt);
+            const int k = pl_pieces(pl_ntk(p, sq, rt), tsplit);
+            if (k > 1) {
+                ex += k - 1;
+                sl += k;
+                ns += 1;
+            }
+        }
+        ex = pl_block_sum(ex, s_red);
+        sl = pl_block_sum(sl, s_red);
+        ns = pl_block_sum(ns, s_red);
+        if (n + ex > p.pf_grid_items || sl > p.pf_slots_max || ns > p.pf_split_max) tsplit = INT32_MAX;
+    }
+    for (int i = tid; i < n; i += PL_THREADS) {
+        int sq, rt;
+        locate(i, sq, rt);
+        const int w = pl_ntk(p, sq, rt);
+        const int k = pl_pieces(w, tsplit);
+        if (k == 1) {
+            atomicAdd(&s_bk[pl_bucket(w)], 1);
+        } else {  // w % k pieces of w / k + 1 tiles, the others of w / k
+            const int big = w % k;
+            if (big) atomicAdd(&s_bk[pl_bucket(w / k + 1)], big);
+            atomicAdd(&s_bk[pl_bucket(w / k)], k - big);
+        }
     }
     __syncthreads();
     // write cursors in descending bucket order: thread t owns buckets
     // B-1-4t .. B-4-4t
+    int total;
     {
         constexpr int PER = PL_BUCKETS / PL_THREADS;
         int c[PER], loc = 0;
@@ -1285,8 +1409,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
             c[k] = s_bk[PL_BUCKETS - 1 - (PER * tid + k)];
             loc += c[k];
         }
-        int tot;
-        int run = pl_block_scan(loc, s_tmp, &tot);
+        int run = pl_block_scan(loc, s_tmp, &total);
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             s_bk[PL_BUCKETS - 1 - (PER * tid + k)] = run;
@@ -1297,11 +1420,76 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     for (int i = tid; i < n; i += PL_THREADS) {
         int sq, rt;
         locate(i, sq, rt);
-        const int pos = atomicAdd(&s_bk[pl_weight(p, sq, rt)], 1);
-        p.pf_seq[pos] = sq;
-        p.pf_rt[pos] = rt;
+        const int w = pl_ntk(p, sq, rt);
+        const int k = pl_pieces(w, tsplit);
+        int slot0 = -1;
+        if (k > 1) {
+            slot0 = atomicAdd(&s_nslot, k);
+            int *e = p.pf_split + 4 * atomicAdd(&s_nsplit, 1);
+            e[0] = sq;
+            e[1] = rt;
+            e[2] = slot0;
+            e[3] = k;
+        }
+        for (int c = 0; c < k; ++c) {
+            const int a = (int)((long long)c * w / k), b = (int)((long long)(c + 1) * w / k);
+            const int pos = atomicAdd(&s_bk[pl_bucket(b - a)], 1);
+            p.pf_seq[pos] = sq;
+            p.pf_rt[pos] = rt;
+            p.pf_kt0[pos] = a;
+            p.pf_kt1[pos] = k > 1 ? b : INT32_MAX;
+            p.pf_slot[pos] = k > 1 ? slot0 + c : -1;
+        }
     }
-    if (tid == 0) p.pf_count[0] = n;
+    __syncthreads();
+    if (tid == 0) {
+        p.pf_count[0] = total;
+        p.pf_count[1] = s_nsplit;
+    }
+}
+
+// Merges the pieces of each split row tile: per row, the pieces' (m, l, O)
+// rescaled to their largest m, O summed and divided by the summed l (0 for a
+// row no piece saw a key of).  A unit is 8 rows of one (split row tile, kv
+// head); 32 lanes per row, four d each.
+template <int ODT>
+__global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p) {
+    const int nsplit = p.pf_count[1];
+    const int units = nsplit * p.Hkv * (PF_ROWS / 8);
+    const int rr = threadIdx.x >> 5, d = 4 * (threadIdx.x & 31);
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const int h = u % p.Hkv;
+        const int t = u / p.Hkv;
+        const int rg = t % (PF_ROWS / 8);
+        const int*e = p.pf_split + 4 * (t / (PF_ROWS / 8));
+        const int s = e[0], rt = e[1], slot0 = e[2], k = e[3];
+        const int q0 = p.qsl[s];
+        const int nrows = (p.qsl[s + 1] - q0) * p.G;
+        const int rl = 8 * rg + rr;          // row inside the tile
+        const int r = PF_ROWS * rt + rl;     // packed row of the sequence
+        if (r >= nrows) continue;
+        float M = -INFINITY;
+        for (int c = 0; c < k; ++c)
+            M = fmaxf(M, p.pf_ml[(((int64_t)(slot0 + c) * p.Hkv + h) * PF_ROWS + rl) * 2]);
+        float L = 0.f;
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        if (M > -INFINITY) {
+            for (int c = 0; c < k; ++c) {
+                const int64_t reg = ((int64_t)(slot0 + c) * p.Hkv + h) * PF_ROWS + rl;
+                const float mc = p.pf_ml[reg * 2];
+                const float wc = mc > -INFINITY ? __builtin_amdgcn_exp2f(mc - M) : 0.f;
+                L = fmaf(wc, p.pf_ml[reg * 2 + 1], L);
+                const float4_t oc = *reinterpret_cast<const float4_t *>(p.pf_o + reg * 128 + d);
+                acc += wc * oc;
+            }
+        }
+        const float inv = L > 0.f ? 1.0f / L : 0.0f;
+        const int j = r / p.G;
+        const int hq = h * p.G + (r - j * p.G);
+        const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, acc[i] * inv);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1330,8 +1518,11 @@ struct Plan {
     int ndc;            // decode classes launched (0..2)
     int dec_rows_max;   // largest decode row bound (0: every sequence is prefill)
     bool need_prefill;
-    int pf_items_max;   // bound on prefill work items (0: no work list)
-    size_t off_items, bytes;
+    int pf_items_max;   // bound on prefill row tiles (0: no work list)
+    int pf_split_max;   // split row tiles (and extra pieces), at most
+    int pf_slots_max;   // partial slots per kv head
+    int pf_grid_items;  // work-list capacity: the prefill grid over Hkv
+    size_t off_items, off_split, off_pml, off_po, bytes;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1376,8 +1567,14 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     pl.need_prefill = max_rows > pl.dec_rows_max;
     // row tiles over all sequences <= sum ceil(n_q * G / 256) <= T*G/256 + B
     const int64_t items = ((int64_t)max(num_tokens, 0) * G + PF_ROWS - 1) / PF_ROWS + num_seqs;
-    pl.pf_items_max = (pl.need_prefill && num_seqs <= PL_MAX_SEQS && items * num_kv_heads < INT32_MAX)
-                          ? (int)items : 0;
+    // a split row tile holds more than pf_ncu / Hkv of the launch's key tiles:
+    // fewer than ceil(CUs / Hkv) of them, with fewer than twice that many pieces
+    const int64_t split = (device_cus() + num_kv_heads - 1) / num_kv_heads;
+    pl.pf_items_max = (pl.need_prefill && num_seqs <= PL_MAX_SEQS &&
+                       (items + split) * num_kv_heads < INT32_MAX) ? (int)items : 0;
+    pl.pf_split_max = pl.pf_items_max ? (int)split : 0;
+    pl.pf_slots_max = 2 * pl.pf_split_max;
+    pl.pf_grid_items = pl.pf_items_max + pl.pf_split_max;
     size_t off = 0;
     for (int k = 0; k < pl.ndc; ++k) {
         DecClass &c = pl.dc[k];
@@ -1389,8 +1586,13 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
         off = c.off_o + align256((size_t)2 * c.nwg * rc * 128 * sizeof(float));
     }
     pl.off_items = off;
-    // work list: a 256-byte header (the item count), then the two item arrays
-    pl.bytes = max(pl.off_items + 256 + align256((size_t)2 * pl.pf_items_max * sizeof(int)), (size_t)256);
+    // work list: a 256-byte header (item count, split row tile count), the
+    // five item arrays, the split list, then the partials of the split pieces
+    pl.off_split = pl.off_items + 256 + align256((size_t)5 * pl.pf_grid_items * sizeof(int));
+    const size_t prow = (size_t)pl.pf_slots_max * num_kv_heads * PF_ROWS;
+    pl.off_pml = pl.off_split + align256((size_t)4 * pl.pf_split_max * sizeof(int));
+    pl.off_po = pl.off_pml + align256(prow * 2 * sizeof(float));
+    pl.bytes = max(pl.off_po + align256(prow * 128 * sizeof(float)), (size_t)256);
     return pl;
 }
 
@@ -1425,8 +1627,10 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
     if (pl.need_prefill) {
         const int rows = max_query_len * p.G;
         const int tiles = (rows + PF_ROWS - 1) / PF_ROWS;
-        const dim3 grid = p.pf_seq ? dim3(pl.pf_items_max * num_kv_heads) : dim3(tiles * num_kv_heads, num_seqs);
+        const dim3 grid = p.pf_seq ? dim3(pl.pf_grid_items * num_kv_heads) : dim3(tiles * num_kv_heads, num_seqs);
         attn_prefill_kernel<QDT, ODT, false, false><<<grid, 64 * PF_WAVES, 0, stream>>>(p);
+        if (p.pf_seq && pl.pf_split_max)  // returns at once when the plan split nothing
+            attn_prefill_combine_kernel<ODT><<<device_cus(), 256, 0, stream>>>(p);
     }
     return hipGetLastError();
 }
@@ -1530,9 +1734,20 @@ hipError_t paged_attention_impl(
     char *ws = static_cast<char *>(workspace);
     p.num_seqs = num_seqs;
     p.pf_items_max = pl.pf_items_max;
+    p.pf_grid_items = pl.pf_grid_items;
+    p.pf_ncu = device_cus();
+    p.pf_split_max = pl.pf_split_max;
+    p.pf_slots_max = pl.pf_slots_max;
+    const int ni = pl.pf_grid_items;
     p.pf_count = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_items) : nullptr;
     p.pf_seq = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_items + 256) : nullptr;
-    p.pf_rt = pl.pf_items_max ? p.pf_seq + pl.pf_items_max : nullptr;
+    p.pf_rt = pl.pf_items_max ? p.pf_seq + ni : nullptr;
+    p.pf_kt0 = pl.pf_items_max ? p.pf_seq + 2 * ni : nullptr;
+    p.pf_kt1 = pl.pf_items_max ? p.pf_seq + 3 * ni : nullptr;
+    p.pf_slot = pl.pf_items_max ? p.pf_seq + 4 * ni : nullptr;
+    p.pf_split = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_split) : nullptr;
+    p.pf_ml = pl.pf_items_max ? reinterpret_cast<float *>(ws + pl.off_pml) : nullptr;
+    p.pf_o = pl.pf_items_max ? reinterpret_cast<float *>(ws + pl.off_po) : nullptr;
     // decode workspace pointers are set per decode class in launch_all
     p.ws_hdr = nullptr;
     p.ws_pre = nullptr;
