@@ -785,6 +785,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 #endif
 constexpr int PF_WAVES = GFA_PF_WAVES;        // 8 (2 waves per SIMD) or 4 (1 wave per SIMD)
 constexpr int PF_ROWS = 32 * PF_WAVES;
+#ifndef GFA_PF_SKIP
+#define GFA_PF_SKIP 1
+#endif
 #ifndef GFA_PF_TK
 #define GFA_PF_TK 64
 #endif
@@ -1041,7 +1044,12 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     // mode: 0 = fetch tile kt+2 and dequantize tile kt+1 (a full tile),
     //       1 = same, tile kt+1 being the last (tail) tile,
     //       2 = nothing left to fetch or dequantize
-    auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode) {
+    // A wave whose 32 rows are all past the sequence's rows (the last row tile
+    // of a sequence) only fetches and dequantizes: the workgroup runs such
+    // tiles through a second copy of the tile loop (guard), so full row tiles
+    // keep the unbranched schedule.
+    const bool wact = row0 + 32 * w < nrows;  // uniform over the wave
+    auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode, auto guard) {
         // odd: kt & 1 (compile time) - read stages kt&1, write stages (kt+1)&1
         const uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
         const uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
@@ -1073,6 +1081,14 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
             for (int kk = 0; kk < 8; ++kk) {
                 const half8_t a = *reinterpret_cast<const half8_t *>(kst + kread + 32 * st * PF_KPITCH + 32 * kk);
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
+            }
+        }
+        // past here an idle wave skips (the branch after the QK MFMAs keeps
+        // the dequant of the next tile interleaved with them)
+        if constexpr (decltype(guard)::value) {
+            if (!wact) {
+                __syncthreads();
+                return;
             }
         }
         const int kbase_t = PF_TK * (kt + ktb);
@@ -1170,31 +1186,41 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
         }
     }
     __syncthreads();
-    // Main loop: pairs of tiles whose dequantized successors are full tiles.
-    // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2.
-    int kt = 0;
-    for (; kt + 3 < ntk; kt += 2) {
-        step(kt, r0, r1, Even{}, Full{});
-        step(kt + 1, r1, r0, Odd{}, Full{});
-        if (kt + 2 - cbase >= 64) {  // slide the page windows (uniform)
-            cbase += 64;
-            pw0 = pw1;
-            pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
-            ready(pw1);
+    auto tiles = [&](auto g) {
+        // Main loop: pairs of tiles whose dequantized successors are full tiles.
+        // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2.
+        int kt = 0;
+        for (; kt + 3 < ntk; kt += 2) {
+            step(kt, r0, r1, Even{}, Full{}, g);
+            step(kt + 1, r1, r0, Odd{}, Full{}, g);
+            if (kt + 2 - cbase >= 64) {  // slide the page windows (uniform)
+                cbase += 64;
+                pw0 = pw1;
+                pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
+                ready(pw1);
+            }
         }
-    }
-    // the last 1-3 tiles (uniform)
-    const int rem = ntk - kt;
-    if (rem == 3) {
-        step(kt, r0, r1, Even{}, Full{});
-        step(kt + 1, r1, r0, Odd{}, Tail{});
-        step(kt + 2, r0, r1, Even{}, Last{});
-    } else if (rem == 2) {
-        step(kt, r0, r1, Even{}, Tail{});
-        step(kt + 1, r1, r0, Odd{}, Last{});
-    } else if (rem == 1) {
-        step(kt, r0, r1, Even{}, Last{});
-    }
+        // the last 1-3 tiles (uniform)
+        const int rem = ntk - kt;
+        if (rem == 3) {
+            step(kt, r0, r1, Even{}, Full{}, g);
+            step(kt + 1, r1, r0, Odd{}, Tail{}, g);
+            step(kt + 2, r0, r1, Even{}, Last{}, g);
+        } else if (rem == 2) {
+            step(kt, r0, r1, Even{}, Tail{}, g);
+            step(kt + 1, r1, r0, Odd{}, Last{}, g);
+        } else if (rem == 1) {
+            step(kt, r0, r1, Even{}, Last{}, g);
+        }
+    };
+#if GFA_PF_SKIP == 2
+    if (row0 + PF_ROWS <= nrows) tiles(std::false_type{});
+    else tiles(std::true_type{});
+#elif GFA_PF_SKIP == 1
+    tiles(std::true_type{});
+#else
+    tiles(std::false_type{});
+#endif
 
     // normalise and store: register e of d-tile dt is d = 32dt + 8(e/4) + 4hb + e%4
     {
