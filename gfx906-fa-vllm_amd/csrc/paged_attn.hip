@@ -86,7 +86,7 @@ struct AttnParams {
     int pf_items_max;   // row tiles, at most
     int pf_grid_items;  // work-list capacity (the grid): row tiles + extra pieces
     int pf_ncu;         // CUs the split targets
-    int pf_split_max;   // split row tiles, at most (also the extra pieces)
+    int pf_split_max;   // split row tiles, at most
     int pf_slots_max;   // partial slots per kv head
     int *pf_split;      // split row tiles: (sequence, row tile, first slot, pieces) each
     float *pf_ml, *pf_o;  // partials: [slot][Hkv][PF_ROWS] x (m, l) and x 128
@@ -1361,11 +1361,15 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     // most tsplit.  tsplit starts at one CU's share of the launch's key tiles
     // (all row tiles x kv heads over pf_ncu; at least PF_SPLIT_MIN): split row
     // tiles then number < pf_ncu / Hkv, their pieces < 2 pf_ncu / Hkv, and the
-    // extra work items < pf_ncu / Hkv; past the workspace's bounds
-    // (impossible by these sums) nothing is split.  With fewer row tiles than
-    // m = pf_ncu / Hkv, tsplit rises to the smallest value whose pieces fit
-    // one workgroup per CU (sum of pieces <= m): a few pieces over m would
-    // start a second round of workgroups and double the launch's time.
+    // extra work items < pf_ncu / Hkv.
+    // With few row tiles (n <= 2m, m = pf_ncu / Hkv: one or two rounds of
+    // workgroups) the rounds decide the time instead: a few workgroups over a
+    // multiple of the CU count start another round.  tsplit then rises to the
+    // smallest value whose pieces fit R rounds (sum of pieces <= R m): R = 1
+    // for n < m, else one round more than the unsplit row tiles take, kept
+    // only if R rounds of tsplit beat the unsplit rounds of the longest row
+    // tile by 10 %.  Pieces then number <= 3m and split row tiles <= 2m.
+    // Past the workspace's bounds (impossible by these sums) nothing is split.
     long long wsum = 0;
     for (int i = tid; i < n; i += PL_THREADS) {
         int sq, rt;
@@ -1375,22 +1379,41 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     const long long W = pl_block_sum(wsum, s_red);
     long long tl = max((W * p.Hkv + p.pf_ncu - 1) / p.pf_ncu, (long long)PF_SPLIT_MIN);
     const int m = p.pf_ncu / p.Hkv;
-    if (n < m && n <= PL_THREADS && p.pf_slots_max > 0) {
+    if (m > 0 && n > 0 && n <= 2 * m && n <= PL_THREADS && p.pf_slots_max > 0) {
         int wt = 0;  // thread t holds row tile t's key tiles
         if (tid < n) {
             int sq, rt;
             locate(tid, sq, rt);
             wt = pl_ntk(p, sq, rt);
         }
-        // pieces(tsplit) is non-increasing; at hi it sums to <= W / hi + n <= m
-        long long lo = tl, hi = max(tl, (W + (m - n) - 1) / (m - n));
+        const int rounds0 = (n + m - 1) / m;       // unsplit, all row tiles alike
+        const int R = n < m ? 1 : rounds0 + 1;
+        const long long cap = (long long)R * m;   // > n
+        // pieces(tsplit) is non-increasing, >= W / tsplit, and at hi sums to
+        // <= W / hi + n <= cap
+        long long lo = max((W + cap - 1) / cap, (long long)PF_SPLIT_MIN);
+        long long hi = max(lo, (W + (cap - n) - 1) / (cap - n));
         while (lo < hi) {
             const long long mid = (lo + hi) >> 1;
             const long long P = pl_block_sum(tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0, s_red);
-            if (P <= m) hi = mid;
+            if (P <= cap) hi = mid;
             else lo = mid + 1;
         }
-        tl = lo;
+        if (R == 1) {
+            tl = lo;
+        } else {
+            // longest row tile: a block max through the sum's reduction tree
+            long long v = wt;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v = max(v, (long long)__shfl_xor(v, off));
+            __syncthreads();
+            if ((tid & 63) == 0) s_red[tid >> 6] = v;
+            __syncthreads();
+            long long wmax = 0;
+#pragma unroll
+            for (int i = 0; i < PL_THREADS / 64; ++i) wmax = max(wmax, s_red[i]);
+            if (10 * R * lo < 9LL * rounds0 * wmax) tl = lo;
+        }
     }
     int tsplit = p.pf_slots_max > 0 ? (int)min(tl, (long long)INT32_MAX) : INT32_MAX;
     if (tsplit < INT32_MAX) {
@@ -1545,7 +1568,7 @@ struct Plan {
     int dec_rows_max;   // largest decode row bound (0: every sequence is prefill)
     bool need_prefill;
     int pf_items_max;   // bound on prefill row tiles (0: no work list)
-    int pf_split_max;   // split row tiles (and extra pieces), at most
+    int pf_split_max;   // split row tiles, at most
     int pf_slots_max;   // partial slots per kv head
     int pf_grid_items;  // work-list capacity: the prefill grid over Hkv
     size_t off_items, off_split, off_pml, off_po, bytes;
@@ -1595,12 +1618,14 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     const int64_t items = ((int64_t)max(num_tokens, 0) * G + PF_ROWS - 1) / PF_ROWS + num_seqs;
     // a split row tile holds more than pf_ncu / Hkv of the launch's key tiles:
     // fewer than ceil(CUs / Hkv) of them, with fewer than twice that many pieces
+    // (a few row tiles, n <= 2 ceil(CUs / Hkv), may instead be cut into up to
+    // three rounds of workgroups: <= 3 ceil(CUs / Hkv) pieces in all)
     const int64_t split = (device_cus() + num_kv_heads - 1) / num_kv_heads;
     pl.pf_items_max = (pl.need_prefill && num_seqs <= PL_MAX_SEQS &&
-                       (items + split) * num_kv_heads < INT32_MAX) ? (int)items : 0;
-    pl.pf_split_max = pl.pf_items_max ? (int)split : 0;
-    pl.pf_slots_max = 2 * pl.pf_split_max;
-    pl.pf_grid_items = pl.pf_items_max + pl.pf_split_max;
+                       (items + 3 * split) * num_kv_heads < INT32_MAX) ? (int)items : 0;
+    pl.pf_split_max = pl.pf_items_max ? (int)(2 * split) : 0;
+    pl.pf_slots_max = pl.pf_items_max ? (int)(3 * split) : 0;
+    pl.pf_grid_items = pl.pf_items_max ? (int)max(items + split, 3 * split) : 0;
     size_t off = 0;
     for (int k = 0; k < pl.ndc; ++k) {
         DecClass &c = pl.dc[k];

@@ -92,10 +92,10 @@ def test_workspace_size_plan():
     assert gfx906_fa.workspace_size(8, 40, 6, 1, 5, 131077) > gfx906_fa.workspace_size(8, 8, 6, 1, 1, 131077)
     # independent of the context length (stream-K shares work per wave)
     assert gfx906_fa.workspace_size(32, 32, 48, 8, 1, 1 << 20) == b
-    # a prefill launch also holds the partials of split row tiles: 2 ceil(CUs / Hkv)
+    # a prefill launch also holds the partials of split row tiles: 3 ceil(CUs / Hkv)
     # slots per kv head of 256 rows x (128 + 2) floats (256 CUs without a GPU)
     pf = gfx906_fa.workspace_size(1, 50, 48, 8, 50, 65586)
-    assert pf >= 2 * 32 * 8 * 256 * 130 * 4
+    assert pf >= 3 * 32 * 8 * 256 * 130 * 4
     assert gfx906_fa.workspace_size(1, 50, 48, 8, 50, 1 << 20) == pf
 
 

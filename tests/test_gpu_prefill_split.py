@@ -5,7 +5,8 @@ are few and long - a prefix-cached chunk of tens to hundreds of tokens after a
 long context, or a batch of such - has its row tiles cut into key ranges that
 separate workgroups run; a combine kernel merges their partial (m, l, O).  The
 shapes below make the device-side plan split: one row tile, several, a partial
-last row tile, a batch mixing decode and prefill sequences, causal from key 0,
+last row tile, row tiles filling one to two rounds of workgroups cut to fill
+one more, a batch mixing decode and prefill sequences, causal from key 0,
 non-causal, every output dtype, and a HIP graph replayed with sequence lengths
 that change the split.  Each case is checked against the oracle."""
 import math
@@ -29,6 +30,7 @@ CASES = [
     ("mixed_decode", [5000, 3000 + 100, 900, 70], [1, 100, 3, 70], 16, 2),
     ("gqa4_chunk200_ctx12k", [12000 + 200], [200], 32, 8),
     ("mqa_fresh2048", [2048], [2048], 8, 1),                 # causal from key 0, 64 row tiles
+    ("two_rounds_16x100_ctx4k", [4096 + 100] * 16, [100] * 16, 48, 8),  # 48 row tiles: cut for 3 rounds
 ]
 
 
