@@ -31,7 +31,9 @@ Also reported on the same JSON line:
                   batch per call, eager vs replayed from a HIP graph; the
                   output epilogue: the reference's fp32 BSHD -> BHSD ->
                   model-dtype copies timed at cfg3's output size (here the
-                  kernels write the model dtype in place).
+                  kernels write the model dtype in place); prefix chunks:
+                  short prefills on long cached prefixes (their row tiles
+                  split over the keys), per pass.
   cpu_baseline  - the reference's PyTorch CPU path (paged gather + dequantize
                   + fp32 SDPA, oracle/cpu_baseline.py) on whole cfg2
                   sequences, repeated for a ~10 s budget, same GB/s accounting.
@@ -177,6 +179,28 @@ def output_epilogue_ms(dev) -> dict:
     del o32, o16
     torch.cuda.empty_cache()
     return {"workload": "cfg3 output, 32768 x 48 x 128", "reference_epilogue_ms": round(ms, 4), "here_ms": 0.0}
+
+
+def prefix_chunk_times(dev) -> dict:
+    """Short prefills on long cached prefixes (prefix caching), 48/8, fp16
+    out: one attention pass each.  The prefill plan splits their row tiles
+    over the keys; TFLOP/s counts the visible keys of the real rows only."""
+    import torch
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+    res = {"workload": "48/8, fp16 out, paged Q8 cache"}
+    for name, B, ctx, nq in (("1x(65536+50)", 1, 65536, 50), ("8x(32768+12)", 8, 32768, 12),
+                             ("1x(129024+2048)", 1, 129024, 2048)):
+        b = W.build_batch([ctx + nq] * B, [nq] * B, 48, 8, seed=7, device=dev, host_values=False)
+        o = torch.empty((b.num_tokens, b.Hq, b.D), dtype=torch.float16, device=dev)
+        ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(
+            b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len), dev)
+        ms = timed(_attn_fn(b, o, ws), 10, 3)
+        res[name] = {"us": round(ms * 1e3, 1), "tflops": round(b.flops() / (ms * 1e-3) / 1e12, 1),
+                     "cache_gbs": round(b.kv_bytes() / (ms * 1e-3) / 1e9, 1)}
+        del b, o, ws
+        torch.cuda.empty_cache()
+    return res
 
 
 def _attn_fn(b, out, ws):
@@ -423,7 +447,8 @@ def main() -> int:
 
     if graph is not None:
         res["next_rows"] = {"graph_replay": graph,
-                            "output_epilogue": output_epilogue_ms(dev)}
+                            "output_epilogue": output_epilogue_ms(dev),
+                            "prefix_chunks": prefix_chunk_times(dev)}
 
     if args.calib_copy_mib:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE

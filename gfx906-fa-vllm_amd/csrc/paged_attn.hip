@@ -1228,6 +1228,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
         const float l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         if (slot >= 0) {  // a piece of a split row tile: unnormalised O, m (log2), l
             const int rl = 32 * w + (lane & 31);
+            if (!rvalid) return;  // the combine reads the sequence's rows only
             const int64_t reg = (int64_t)slot * Hkv + h;
             float *po = p.pf_o + (reg * PF_ROWS + rl) * 128 + 4 * hb;
 #pragma unroll
@@ -1268,21 +1269,28 @@ constexpr int PL_BUCKETS = 4096;   // key tiles per item, clamped (256K keys)
 #endif
 constexpr int PF_SPLIT_MIN = GFA_PF_SPLIT_MIN;  // a split row tile's pieces: at least this many tiles
 
-// exclusive scan of v over the workgroup; *total receives the sum
+// exclusive scan of v over the workgroup; *total receives the sum (a scan
+// inside each wave, then the waves' totals through tmp)
 __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
-    const int tid = threadIdx.x;
-    tmp[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < PL_THREADS; off <<= 1) {
-        const int a = tid >= off ? tmp[tid - off] : 0;
-        __syncthreads();
-        tmp[tid] += a;
-        __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
     }
-    const int incl = tmp[tid];
-    *total = tmp[PL_THREADS - 1];
+    __syncthreads();  // tmp[] of a previous call has been read
+    if (lane == 63) tmp[wv] = x;
     __syncthreads();
-    return incl - v;
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < PL_THREADS / 64; ++i) {
+        const int t = tmp[i];
+        before += i < wv ? t : 0;
+        tot += t;
+    }
+    *total = tot;
+    return before + x - v;
 }
 
 __device__ __forceinline__ int pl_tiles(const AttnParams &p, int s) {
@@ -1318,6 +1326,19 @@ __device__ __forceinline__ long long pl_block_sum(long long v, long long *red) {
     return t;
 }
 
+// max of v over the workgroup (every thread receives it)
+__device__ __forceinline__ long long pl_block_max(long long v, long long *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, (long long)__shfl_xor(v, off));
+    __syncthreads();  // red[] of a previous call has been read
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    long long t = red[0];
+#pragma unroll
+    for (int i = 1; i < PL_THREADS / 64; ++i) t = max(t, red[i]);
+    return t;
+}
+
 // Pieces row tile of w key tiles is cut into when pieces hold at most tsplit
 // tiles; piece c of k covers tiles [c*w/k, (c+1)*w/k).
 __device__ __forceinline__ int pl_pieces(int w, int tsplit) { return w > tsplit ? (w + tsplit - 1) / tsplit : 1; }
@@ -1325,7 +1346,7 @@ __device__ __forceinline__ int pl_pieces(int w, int tsplit) { return w > tsplit 
 __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) {
     __shared__ int s_pre[PL_MAX_SEQS + 1];  // exclusive prefix of row tiles per sequence
     __shared__ int s_bk[PL_BUCKETS];        // bucket counts, then write cursors
-    __shared__ int s_tmp[PL_THREADS];
+    __shared__ int s_tmp[PL_THREADS / 64];
     __shared__ long long s_red[PL_THREADS / 64];
     __shared__ int s_nsplit, s_nslot;
     const int B = p.num_seqs, tid = threadIdx.x;
@@ -1370,15 +1391,19 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     // only if R rounds of tsplit beat the unsplit rounds of the longest row
     // tile by 10 %.  Pieces then number <= 3m and split row tiles <= 2m.
     // Past the workspace's bounds (impossible by these sums) nothing is split.
-    long long wsum = 0;
+    long long wsum = 0, wmx = 0;
     for (int i = tid; i < n; i += PL_THREADS) {
         int sq, rt;
         locate(i, sq, rt);
-        wsum += pl_ntk(p, sq, rt);
+        const int w = pl_ntk(p, sq, rt);
+        wsum += w;
+        wmx = max(wmx, (long long)w);
     }
     const long long W = pl_block_sum(wsum, s_red);
+    const long long wmax = pl_block_max(wmx, s_red);  // the longest row tile
     long long tl = max((W * p.Hkv + p.pf_ncu - 1) / p.pf_ncu, (long long)PF_SPLIT_MIN);
     const int m = p.pf_ncu / p.Hkv;
+    bool proven = false;  // the bisection's sums bound the plan: no check pass
     if (m > 0 && n > 0 && n <= 2 * m && n <= PL_THREADS && p.pf_slots_max > 0) {
         int wt = 0;  // thread t holds row tile t's key tiles
         if (tid < n) {
@@ -1399,24 +1424,13 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
             if (P <= cap) hi = mid;
             else lo = mid + 1;
         }
-        if (R == 1) {
+        if (R == 1 || 10 * R * lo < 9LL * rounds0 * wmax) {
             tl = lo;
-        } else {
-            // longest row tile: a block max through the sum's reduction tree
-            long long v = wt;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v = max(v, (long long)__shfl_xor(v, off));
-            __syncthreads();
-            if ((tid & 63) == 0) s_red[tid >> 6] = v;
-            __syncthreads();
-            long long wmax = 0;
-#pragma unroll
-            for (int i = 0; i < PL_THREADS / 64; ++i) wmax = max(wmax, s_red[i]);
-            if (10 * R * lo < 9LL * rounds0 * wmax) tl = lo;
+            proven = true;  // pieces <= R m <= 3m, split row tiles <= n <= 2m
         }
     }
-    int tsplit = p.pf_slots_max > 0 ? (int)min(tl, (long long)INT32_MAX) : INT32_MAX;
-    if (tsplit < INT32_MAX) {
+    int tsplit = (p.pf_slots_max > 0 && tl < wmax) ? (int)tl : INT32_MAX;  // else nothing is cut
+    if (tsplit < INT32_MAX && !proven) {
         long long ex = 0, sl = 0, ns = 0;
         for (int i = tid; i < n; i += PL_THREADS) {
             int sq, rt;
@@ -1497,47 +1511,79 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     }
 }
 
-// Merges the pieces of each split row tile: per row, the pieces' (m, l, O)
-// rescaled to their largest m, O summed and divided by the summed l (0 for a
-// row no piece saw a key of).  A unit is 8 rows of one (split row tile, kv
-// head); 32 lanes per row, four d each.
+// Merges the pieces of each split row tile: per row, an online merge of the
+// pieces' (m, l, O) - the running sums rescaled to the largest m so far - and
+// O divided by l at the end (0 for a row no piece saw a key of).  A unit is 16
+// rows of one (split row tile, kv head): 32 lanes per row, four d each, two
+// rows per thread.  A thread issues the loads of both rows for four pieces
+// before merging them, so they are in flight together.
 template <int ODT>
 __global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p) {
+    constexpr int RPU = 16, U = 4;
     const int nsplit = p.pf_count[1];
-    const int units = nsplit * p.Hkv * (PF_ROWS / 8);
+    const int units = nsplit * p.Hkv * (PF_ROWS / RPU);
     const int rr = threadIdx.x >> 5, d = 4 * (threadIdx.x & 31);
+    const int64_t rstep = (int64_t)p.Hkv * PF_ROWS;  // piece c -> c + 1
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const int h = u % p.Hkv;
         const int t = u / p.Hkv;
-        const int rg = t % (PF_ROWS / 8);
-        const int*e = p.pf_split + 4 * (t / (PF_ROWS / 8));
+        const int rg = t % (PF_ROWS / RPU);
+        const int *e = p.pf_split + 4 * (t / (PF_ROWS / RPU));
         const int s = e[0], rt = e[1], slot0 = e[2], k = e[3];
         const int q0 = p.qsl[s];
         const int nrows = (p.qsl[s + 1] - q0) * p.G;
-        const int rl = 8 * rg + rr;          // row inside the tile
-        const int r = PF_ROWS * rt + rl;     // packed row of the sequence
-        if (r >= nrows) continue;
-        float M = -INFINITY;
-        for (int c = 0; c < k; ++c)
-            M = fmaxf(M, p.pf_ml[(((int64_t)(slot0 + c) * p.Hkv + h) * PF_ROWS + rl) * 2]);
-        float L = 0.f;
-        float4_t acc = {0.f, 0.f, 0.f, 0.f};
-        if (M > -INFINITY) {
-            for (int c = 0; c < k; ++c) {
-                const int64_t reg = ((int64_t)(slot0 + c) * p.Hkv + h) * PF_ROWS + rl;
-                const float mc = p.pf_ml[reg * 2];
-                const float wc = mc > -INFINITY ? __builtin_amdgcn_exp2f(mc - M) : 0.f;
-                L = fmaf(wc, p.pf_ml[reg * 2 + 1], L);
-                const float4_t oc = *reinterpret_cast<const float4_t *>(p.pf_o + reg * 128 + d);
-                acc += wc * oc;
-            }
-        }
-        const float inv = L > 0.f ? 1.0f / L : 0.0f;
-        const int j = r / p.G;
-        const int hq = h * p.G + (r - j * p.G);
-        const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d;
+        float M[2], L[2];
+        float4_t acc[2];
+        int64_t reg0[2];
+        bool ok[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, acc[i] * inv);
+        for (int i = 0; i < 2; ++i) {
+            const int rl = RPU * rg + rr + 8 * i;  // row inside the tile
+            ok[i] = PF_ROWS * rt + rl < nrows;
+            reg0[i] = ((int64_t)slot0 * p.Hkv + h) * PF_ROWS + rl;
+            M[i] = -INFINITY;
+            L[i] = 0.f;
+            acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        for (int c0 = 0; c0 < k; c0 += U) {
+            float2_t ml[2][U];
+            float4_t oc[2][U];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < U; ++j) {
+                    const int64_t reg = reg0[i] + (c0 + j) * rstep;
+                    const bool in = ok[i] && c0 + j < k;
+                    ml[i][j] = in ? *reinterpret_cast<const float2_t *>(p.pf_ml + reg * 2) : float2_t{-INFINITY, 0.f};
+                    oc[i][j] = in ? *reinterpret_cast<const float4_t *>(p.pf_o + reg * 128 + d)
+                                  : float4_t{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < U; ++j) {
+                    const float mc = ml[i][j][0];
+                    if (mc > -INFINITY) {
+                        const float mn = fmaxf(M[i], mc);
+                        const float a = __builtin_amdgcn_exp2f(M[i] - mn);  // 0 while M is -inf
+                        const float b = __builtin_amdgcn_exp2f(mc - mn);
+                        L[i] = fmaf(L[i], a, b * ml[i][j][1]);
+                        acc[i] = acc[i] * a + b * oc[i][j];
+                        M[i] = mn;
+                    }
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (!ok[i]) continue;
+            const int r = PF_ROWS * rt + RPU * rg + rr + 8 * i;
+            const float inv = L[i] > 0.f ? 1.0f / L[i] : 0.0f;
+            const int j = r / p.G;
+            const int hq = h * p.G + (r - j * p.G);
+            const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) store_out<ODT>(p.out, ob + x, acc[i][x] * inv);
+        }
     }
 }
 
