@@ -72,6 +72,20 @@ def test_split_prefill_output_dtypes(dt, extra):
     assert_close(to_np_f32(out), batch_oracle(b), extra=extra)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_split_prefill_query_dtypes(dtype):
+    """bf16 and fp32 models: the query read and the output written in the
+    model dtype by the split pieces and the merge."""
+    need_gpu()
+    announce(f"prefill split query={dtype}")
+    b = W.build_batch([5000 + 60], [60], 48, 8, dtype=dtype, seed=94)
+    out = W.attention(b)
+    torch.cuda.synchronize()
+    assert out.dtype == b.query.dtype
+    extra = {"bf16": 2.0 ** -8, "f32": 0.0}[dtype]
+    assert_close(to_np_f32(out), batch_oracle(b), extra=extra)
+
+
 def test_split_prefill_non_causal():
     """causal=0: every query row sees all seq_len keys (one-row oracle calls
     over the whole sequence)."""
