@@ -7,7 +7,8 @@ separate workgroups run; a combine kernel merges their partial (m, l, O).  The
 shapes below make the device-side plan split: one row tile, several, a partial
 last row tile, row tiles filling one to two rounds of workgroups cut to fill
 one more, a batch mixing decode and prefill sequences, causal from key 0,
-non-causal, every output dtype, and a HIP graph replayed with sequence lengths
+non-causal, a chunk inside its sequence (q_abs_offset), every query and
+output dtype, and a HIP graph replayed with sequence lengths
 that change the split.  Each case is checked against the oracle."""
 import math
 
@@ -103,6 +104,28 @@ def test_split_prefill_non_causal():
         for t in range(int(b.qsl[s]), int(b.qsl[s + 1])):
             ref[t] = O.paged_attention_ref(q[t:t + 1], kh, vh, b.block_table_np[s:s + 1],
                                            b.seq_lens[s:s + 1], np.array([0, 1], np.int32), b.scale)[0]
+    assert_close(to_np_f32(out), ref)
+
+
+def test_split_prefill_q_abs_offset():
+    """q_abs_offset: a 40-token chunk at position 5000 of a 9000-token
+    sequence.  The keys past the chunk exist but are masked; the plan cuts
+    the 5040 visible keys only (one-row oracle calls up to each row's bound)."""
+    need_gpu()
+    announce("prefill split q_abs_offset")
+    b = W.build_batch([9000], [40], 48, 8, seed=95)
+    kp, vp = b.planes()
+    qa = 5000
+    out = gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t, b.max_query_len,
+                                    b.max_seq_len, b.scale, out_dtype=torch.float32,
+                                    q_abs_offset=torch.tensor([qa], dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    kh, vh = O.planar_dequant(b.kv_cache.cpu().numpy())
+    q = to_np_f32(b.query)
+    ref = np.zeros(q.shape, np.float64)
+    for t in range(b.num_tokens):
+        ref[t] = O.paged_attention_ref(q[t:t + 1], kh, vh, b.block_table_np[0:1], np.array([qa + t + 1], np.int32),
+                                       np.array([0, 1], np.int32), b.scale)[0]
     assert_close(to_np_f32(out), ref)
 
 
