@@ -1268,6 +1268,9 @@ constexpr int PL_BUCKETS = 4096;   // key tiles per item, clamped (256K keys)
 #define GFA_PF_SPLIT_MIN 16
 #endif
 constexpr int PF_SPLIT_MIN = GFA_PF_SPLIT_MIN;  // a split row tile's pieces: at least this many tiles
+#ifndef GFA_PFC_WGS_PER_CU
+#define GFA_PFC_WGS_PER_CU 4  // split-merge workgroups per CU (more loads in flight)
+#endif
 
 // exclusive scan of v over the workgroup; *total receives the sum (a scan
 // inside each wave, then the waves' totals through tmp)
@@ -1727,7 +1730,7 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
         const dim3 grid = p.pf_seq ? dim3(pl.pf_grid_items * num_kv_heads) : dim3(tiles * num_kv_heads, num_seqs);
         attn_prefill_kernel<QDT, ODT, false, false><<<grid, 64 * PF_WAVES, 0, stream>>>(p);
         if (p.pf_seq && pl.pf_split_max)  // returns at once when the plan split nothing
-            attn_prefill_combine_kernel<ODT><<<device_cus(), 256, 0, stream>>>(p);
+            attn_prefill_combine_kernel<ODT><<<device_cus() * GFA_PFC_WGS_PER_CU, 256, 0, stream>>>(p);
     }
     return hipGetLastError();
 }
