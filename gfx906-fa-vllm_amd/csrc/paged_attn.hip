@@ -706,17 +706,33 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     const int d0 = 4 * dc;
     float m = -INFINITY, l = 0.f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
-    for (int k = wf + sub; k <= wl; k += 8) {
-        const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
-        const int64_t row = (int64_t)sk * p.dec_rows_max + r;
-        const float mk = p.ws_ml[2 * row], lk = p.ws_ml[2 * row + 1];
-        const float4_t ok = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
-        const float mn = fmaxf(m, mk);
-        const float ms = mn == -INFINITY ? 0.0f : mn;
-        const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
-        l = l * a + lk * c;
-        o = o * a + ok * c;
-        m = mn;
+    // group `sub` merges pieces wf + sub, wf + sub + 8, ... in order; the loads
+    // of four of them are issued before they are merged (in flight together)
+    constexpr int CU = 4;
+    for (int k0 = wf + sub; k0 <= wl; k0 += 8 * CU) {
+        float2_t mlk[CU];
+        float4_t ok[CU];
+#pragma unroll
+        for (int i = 0; i < CU; ++i) {
+            const int k = k0 + 8 * i;
+            if (k <= wl) {
+                const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
+                const int64_t row = (int64_t)sk * p.dec_rows_max + r;
+                mlk[i] = *reinterpret_cast<const float2_t *>(p.ws_ml + 2 * row);
+                ok[i] = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CU; ++i) {
+            if (k0 + 8 * i > wl) break;
+            const float mk = mlk[i][0], lk = mlk[i][1];
+            const float mn = fmaxf(m, mk);
+            const float ms = mn == -INFINITY ? 0.0f : mn;
+            const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
+            l = l * a + lk * c;
+            o = o * a + ok[i] * c;
+            m = mn;
+        }
     }
     __shared__ float sm[8][32][6];
     sm[sub][dc][0] = m;
