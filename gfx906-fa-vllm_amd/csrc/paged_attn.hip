@@ -1367,6 +1367,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     __shared__ int s_bk[PL_BUCKETS];        // bucket counts, then write cursors
     __shared__ int s_tmp[PL_THREADS / 64];
     __shared__ long long s_red[PL_THREADS / 64];
+    __shared__ int s_w[PL_THREADS];  // key tiles of row tile i (launches of <= PL_THREADS row tiles)
     __shared__ int s_nsplit, s_nslot;
     const int B = p.num_seqs, tid = threadIdx.x;
     int carry = 0;
@@ -1415,9 +1416,12 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         int sq, rt;
         locate(i, sq, rt);
         const int w = pl_ntk(p, sq, rt);
+        if (n <= PL_THREADS) s_w[i] = w;
         wsum += w;
         wmx = max(wmx, (long long)w);
     }
+    // (the block reductions below order these stores before their reads)
+    auto ntk_of = [&](int i, int sq, int rt) { return n <= PL_THREADS ? s_w[i] : pl_ntk(p, sq, rt); };
     const long long W = pl_block_sum(wsum, s_red);
     const long long wmax = pl_block_max(wmx, s_red);  // the longest row tile
     long long tl = max((W * p.Hkv + p.pf_ncu - 1) / p.pf_ncu, (long long)PF_SPLIT_MIN);
@@ -1425,11 +1429,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     bool proven = false;  // the bisection's sums bound the plan: no check pass
     if (m > 0 && n > 0 && n <= 2 * m && n <= PL_THREADS && p.pf_slots_max > 0) {
         int wt = 0;  // thread t holds row tile t's key tiles
-        if (tid < n) {
-            int sq, rt;
-            locate(tid, sq, rt);
-            wt = pl_ntk(p, sq, rt);
-        }
+        if (tid < n) wt = s_w[tid];
         const int rounds0 = (n + m - 1) / m;       // unsplit, all row tiles alike
         const int R = n < m ? 1 : rounds0 + 1;
         const long long cap = (long long)R * m;   // > n
@@ -1454,7 +1454,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         for (int i = tid; i < n; i += PL_THREADS) {
             int sq, rt;
             locate(i, sq, rt);
-            const int k = pl_pieces(pl_ntk(p, sq, rt), tsplit);
+            const int k = pl_pieces(ntk_of(i, sq, rt), tsplit);
             if (k > 1) {
                 ex += k - 1;
                 sl += k;
@@ -1469,7 +1469,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     for (int i = tid; i < n; i += PL_THREADS) {
         int sq, rt;
         locate(i, sq, rt);
-        const int w = pl_ntk(p, sq, rt);
+        const int w = ntk_of(i, sq, rt);
         const int k = pl_pieces(w, tsplit);
         if (k == 1) {
             atomicAdd(&s_bk[pl_bucket(w)], 1);
@@ -1502,7 +1502,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     for (int i = tid; i < n; i += PL_THREADS) {
         int sq, rt;
         locate(i, sq, rt);
-        const int w = pl_ntk(p, sq, rt);
+        const int w = ntk_of(i, sq, rt);
         const int k = pl_pieces(w, tsplit);
         int slot0 = -1;
         if (k > 1) {
