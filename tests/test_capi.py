@@ -97,6 +97,10 @@ def test_workspace_size_plan():
     pf = gfx906_fa.workspace_size(1, 50, 48, 8, 50, 65586)
     assert pf >= 3 * 32 * 8 * 256 * 130 * 4
     assert gfx906_fa.workspace_size(1, 50, 48, 8, 50, 1 << 20) == pf
+    # kv-head counts that do not divide the CU count round the slots up per head
+    for hkv in (3, 5, 7, 12):
+        need = 3 * (-(-256 // hkv)) * hkv * 256 * 130 * 4
+        assert gfx906_fa.workspace_size(2, 200, 2 * hkv, hkv, 100, 9000) >= need
 
 
 def test_ops_reject_cpu_tensors():
