@@ -29,6 +29,7 @@
 //                        stream-K over all KV sub-pages, equal share per wave
 //   attn_prefill_kernel  sequences with more rows: 128-row workgroups share
 //                        K/V tiles dequantized to fp16 in LDS; 32x32x16 MFMA
+#include <atomic>
 #include <cstdio>
 #include <type_traits>
 
@@ -1641,56 +1642,57 @@ struct Plan {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// CUs of the current device, queried once per device.  Threads may race on
+// the first query of a device; they store the same value, and the relaxed
+// atomics make that race well defined.  256 (MI355X) when no device is
+// visible, so plans and workspace sizes computed on a host without a GPU
+// match the target part.
 int device_cus() {
-    static int cus[64] = {0};
+    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             n = 256;
-        cus[dev] = n;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return n;
 }
 
-Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int max_query_len) {
-    Plan pl;
-    const int G = num_heads / num_kv_heads;
-    const int max_rows = max_query_len * G;
-    const bool uniform = (int64_t)num_tokens == (int64_t)num_seqs * max_query_len;
-    pl.ndc = 0;
-    auto add = [&](int nrg, int lo, int hi) {
-        DecClass &c = pl.dc[pl.ndc++];
-        c.nrg = nrg;
-        c.rows_lo = lo;
-        c.rows_hi = hi;
-        c.nwg = device_cus() * 4 * (nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe) / DEC_NW;
-    };
-    // the two-row-group class takes up to DEC_CHUNK_ROWS rows in 32-row chunks
-    const int hi2 = max_rows <= 32 ? 32 : DEC_CHUNK_ROWS;
-    if (max_rows <= 16) {
-        add(1, 0, 16);
-    } else if (uniform) {
-        if (max_rows <= DEC_CHUNK_ROWS) add(2, 0, hi2);
-    } else {
-        if (G <= 16) add(1, 0, 16);
-        if (G <= DEC_CHUNK_ROWS) add(2, pl.ndc ? 16 : 0, hi2);
-    }
+void plan_add_class(Plan &pl, int nrg, int lo, int hi) {
+    DecClass &c = pl.dc[pl.ndc++];
+    c.nrg = nrg;
+    c.rows_lo = lo;
+    c.rows_hi = hi;
+    c.nwg = device_cus() * 4 * (nrg == 1 ? DecCfg<1>::wpe : DecCfg<2>::wpe) / DEC_NW;
+}
+
+// Prefill work-list bounds and the workspace layout, once the decode classes
+// are chosen.  Every region grows monotonically with num_seqs, num_tokens and
+// the classes' row bounds (the workspace bound below relies on it).
+// pf_seqs: the sequences the row-tile count assumes; force_pf: lay out the
+// work list even where a call would keep the 2-D prefill grid (bound only).
+// allow_split: reserve the partial slots of row tiles split over the keys
+// (without them the plan kernel leaves every row tile whole).
+void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_heads, bool force_pf,
+                 bool allow_split) {
     pl.dec_rows_max = pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0;
-    pl.need_prefill = max_rows > pl.dec_rows_max;
     // row tiles over all sequences <= sum ceil(n_q * G / 256) <= T*G/256 + B
-    const int64_t items = ((int64_t)max(num_tokens, 0) * G + PF_ROWS - 1) / PF_ROWS + num_seqs;
+    const int pf_seqs = min(num_seqs, PL_MAX_SEQS);
+    const int64_t items = (max(num_tokens, (int64_t)0) * G + PF_ROWS - 1) / PF_ROWS + pf_seqs;
     // a split row tile holds more than pf_ncu / Hkv of the launch's key tiles:
     // fewer than ceil(CUs / Hkv) of them, with fewer than twice that many pieces
     // (a few row tiles, n <= 2 ceil(CUs / Hkv), may instead be cut into up to
     // three rounds of workgroups: <= 3 ceil(CUs / Hkv) pieces in all)
     const int64_t split = (device_cus() + num_kv_heads - 1) / num_kv_heads;
-    pl.pf_items_max = (pl.need_prefill && num_seqs <= PL_MAX_SEQS &&
-                       (items + 3 * split) * num_kv_heads < INT32_MAX) ? (int)items : 0;
-    pl.pf_split_max = pl.pf_items_max ? (int)(2 * split) : 0;
-    pl.pf_slots_max = pl.pf_items_max ? (int)(3 * split) : 0;
-    pl.pf_grid_items = pl.pf_items_max ? (int)max(items + split, 3 * split) : 0;
+    const bool pf = force_pf || (pl.need_prefill && num_seqs <= PL_MAX_SEQS &&
+                                 (items + 3 * split) * num_kv_heads < INT32_MAX);
+    const int64_t grid_items = pf ? max(items + split, 3 * split) : 0;
+    pl.pf_items_max = pf ? (int)min(items, (int64_t)INT32_MAX) : 0;
+    pl.pf_split_max = pf && allow_split ? (int)(2 * split) : 0;
+    pl.pf_slots_max = pf && allow_split ? (int)(3 * split) : 0;
+    pl.pf_grid_items = (int)min(grid_items, (int64_t)INT32_MAX);
     size_t off = 0;
     for (int k = 0; k < pl.ndc; ++k) {
         DecClass &c = pl.dc[k];
@@ -1704,11 +1706,50 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     pl.off_items = off;
     // work list: a 256-byte header (item count, split row tile count), the
     // five item arrays, the split list, then the partials of the split pieces
-    pl.off_split = pl.off_items + 256 + align256((size_t)5 * pl.pf_grid_items * sizeof(int));
+    pl.off_split = pl.off_items + 256 + align256((size_t)5 * grid_items * sizeof(int));
     const size_t prow = (size_t)pl.pf_slots_max * num_kv_heads * PF_ROWS;
     pl.off_pml = pl.off_split + align256((size_t)4 * pl.pf_split_max * sizeof(int));
     pl.off_po = pl.off_pml + align256(prow * 2 * sizeof(float));
     pl.bytes = max(pl.off_po + align256(prow * 128 * sizeof(float)), (size_t)256);
+}
+
+Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int max_query_len,
+               bool allow_split = true) {
+    Plan pl;
+    const int G = num_heads / num_kv_heads;
+    const int max_rows = max_query_len * G;
+    const bool uniform = (int64_t)num_tokens == (int64_t)num_seqs * max_query_len;
+    pl.ndc = 0;
+    // the two-row-group class takes up to DEC_CHUNK_ROWS rows in 32-row chunks
+    const int hi2 = max_rows <= 32 ? 32 : DEC_CHUNK_ROWS;
+    if (max_rows <= 16) {
+        plan_add_class(pl, 1, 0, 16);
+    } else if (uniform) {
+        if (max_rows <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, 0, hi2);
+    } else {
+        if (G <= 16) plan_add_class(pl, 1, 0, 16);
+        if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, hi2);
+    }
+    pl.need_prefill = max_rows > (pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0);
+    plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split);
+    return pl;
+}
+
+// A plan whose every workspace region is at least that of any make_plan()
+// call with num_seqs <= max_num_seqs and num_tokens <= max_num_tokens (any
+// max_query_len, any mix of decode and prefill sequences): each decode class
+// a call can have, at its largest row bound (16 rows; 64 for the two-row-group
+// class), and a prefill work list sized for max_num_tokens.  plan_finish's
+// regions are monotone in all of these, and a call's classes are a subset of
+// these classes in the same order.
+Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num_kv_heads, bool allow_split) {
+    Plan pl;
+    const int G = num_heads / num_kv_heads;
+    pl.ndc = 0;
+    if (G <= 16) plan_add_class(pl, 1, 0, 16);
+    if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, DEC_CHUNK_ROWS);
+    pl.need_prefill = true;
+    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split);
     return pl;
 }
 
@@ -1761,6 +1802,34 @@ extern "C" size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int
     (void)max_seq_len;
     if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads) return 0;
     return make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1)).bytes;
+}
+
+extern "C" size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs, int64_t max_num_tokens,
+                                                                int num_heads, int num_kv_heads,
+                                                                int head_size) {
+    (void)head_size;
+    if (max_num_seqs <= 0 || max_num_tokens < 0 || num_kv_heads <= 0 || num_heads <= 0 ||
+        num_heads % num_kv_heads)
+        return 0;
+    return bound_plan(max_num_seqs, max_num_tokens, num_heads, num_kv_heads, true).bytes;
+}
+
+extern "C" int gfx906_fa_amd_device_cus(void) { return device_cus(); }
+
+extern "C" int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tokens, int num_heads,
+                                                       int num_kv_heads, int head_size, int max_query_len,
+                                                       int max_seq_len, int64_t *info, int info_len) {
+    (void)head_size;
+    (void)max_seq_len;
+    if (info == nullptr || num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads)
+        return -1;
+    const Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1));
+    const int64_t v[] = {(int64_t)pl.bytes, pl.ndc, pl.dec_rows_max, pl.need_prefill ? 1 : 0,
+                         pl.pf_items_max, pl.pf_grid_items, pl.pf_split_max, pl.pf_slots_max,
+                         pl.pf_items_max ? (int64_t)pl.off_items : -1, device_cus()};
+    const int n = (int)(sizeof(v) / sizeof(v[0]));
+    for (int i = 0; i < n && i < info_len; ++i) info[i] = v[i];
+    return n;
 }
 
 namespace {

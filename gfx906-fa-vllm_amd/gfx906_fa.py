@@ -75,6 +75,9 @@ def _load():
         "gfx906_fa_amd_rope_cache_write_kv": (I, [P, P, P, I, P, P, I, I64, I, I, I, P, P, P, I, I, I, I, I,
                                                   I64, I64, I64, I64, I64, I64, I64, I64, P]),
         "gfx906_fa_amd_paged_attention_workspace_size": (SZ, [I, I, I, I, I, I, I]),
+        "gfx906_fa_amd_paged_attention_workspace_bound": (SZ, [I, I64, I, I, I]),
+        "gfx906_fa_amd_paged_attention_plan_info": (I, [I, I, I, I, I, I, I, P, I]),
+        "gfx906_fa_amd_device_cus": (I, []),
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
         "gfx906_fa_amd_paged_attention_kv_write": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
@@ -371,6 +374,37 @@ def workspace_size(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads:
                    max_query_len: int, max_seq_len: int, head_size: int = 128) -> int:
     return int(_load().gfx906_fa_amd_paged_attention_workspace_size(
         num_seqs, num_tokens, num_heads, num_kv_heads, head_size, max_query_len, max_seq_len))
+
+
+def workspace_bound(max_num_seqs: int, max_num_tokens: int, num_heads: int, num_kv_heads: int,
+                    head_size: int = 128) -> int:
+    """Workspace bytes covering every ``paged_attention`` call with at most
+    max_num_seqs sequences and max_num_tokens query tokens, whatever their
+    query lengths and mix (decode, verify, prefill)."""
+    return int(_load().gfx906_fa_amd_paged_attention_workspace_bound(
+        int(max_num_seqs), int(max_num_tokens), num_heads, num_kv_heads, head_size))
+
+
+PLAN_FIELDS = ("bytes", "decode_classes", "dec_rows_max", "prefill", "pf_items_max", "pf_grid_items",
+               "pf_split_max", "pf_slots_max", "pf_header_offset", "cus")
+
+
+def plan_info(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int, max_query_len: int,
+              max_seq_len: int, head_size: int = 128) -> dict:
+    """The launch plan of a call shape (see PLAN_FIELDS).  ``pf_header_offset``
+    is where, in the workspace, the call leaves its prefill work-list header:
+    int32 item count, int32 count of row tiles split over the keys."""
+    buf = (ctypes.c_int64 * len(PLAN_FIELDS))()
+    n = _load().gfx906_fa_amd_paged_attention_plan_info(num_seqs, num_tokens, num_heads, num_kv_heads,
+                                                         head_size, max_query_len, max_seq_len, buf,
+                                                         len(PLAN_FIELDS))
+    _check(n == len(PLAN_FIELDS), f"plan_info: invalid shape (returned {n})")
+    return dict(zip(PLAN_FIELDS, (int(v) for v in buf)))
+
+
+def device_cus() -> int:
+    """CUs of the current device the plans target (256 without a device)."""
+    return int(_load().gfx906_fa_amd_device_cus())
 
 
 def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,

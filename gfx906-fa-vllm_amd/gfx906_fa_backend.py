@@ -69,16 +69,13 @@ class Gfx906FAMetadata:
     common_prefix_len: int = 0
 
 
-def workspace_upper_bound(max_num_seqs: int, max_query_len: int = 16) -> int:
+def workspace_upper_bound(max_num_seqs: int, max_num_tokens: int, heads) -> int:
     """Attention workspace that covers every batch of up to max_num_seqs
-    sequences of up to max_query_len tokens (the workspace does not depend on
-    context lengths): the largest of a uniform 32-row decode batch, a mixed
-    batch using both decode classes and a prefill work list, and a uniform
-    batch that goes to the prefill kernel."""
-    B, q = max_num_seqs, max(int(max_query_len), 2)
-    return max(gfx906_fa.workspace_size(B, B, 32, 1, 1, 1),
-               gfx906_fa.workspace_size(B, B * q - 1, 16, 1, q, 1),
-               gfx906_fa.workspace_size(B, B * q, 128, 1, q, 1))
+    sequences and max_num_tokens query tokens - any query lengths, any mix of
+    decode, speculative-verify and prefill sequences, any context - for each
+    layer shape (num_heads, num_kv_heads) in ``heads``."""
+    return max((gfx906_fa.workspace_bound(max_num_seqs, max_num_tokens, hq, hkv) for hq, hkv in heads),
+               default=0)
 
 
 class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
@@ -92,12 +89,25 @@ class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
                  vllm_config: VllmConfig, device: torch.device):
         super().__init__(kv_cache_spec, layer_names, vllm_config, device)
         self.block_size = kv_cache_spec.block_size
-        # reserve the shared workspace before any capture, so forward() never
-        # allocates inside a graph
+        # Reserve the shared workspace before any capture, so forward() never
+        # allocates inside a graph: the bound over the scheduler's batch
+        # limits for every layer shape seen (the Impls are built with the
+        # model, before the builders).
         sched = getattr(vllm_config, "scheduler_config", None)
         max_seqs = getattr(sched, "max_num_seqs", None)
-        if isinstance(max_seqs, int) and max_seqs > 0 and torch.device(device).type == "cuda":
-            Gfx906FAImpl.reserve_workspace(workspace_upper_bound(max_seqs), torch.device(device))
+        max_tokens = getattr(sched, "max_num_batched_tokens", None)
+        heads = set(Gfx906FAImpl._layer_heads)
+        hkv = getattr(kv_cache_spec, "num_kv_heads", None)
+        model_config = getattr(vllm_config, "model_config", None)
+        if model_config is not None and isinstance(hkv, int) and hkv > 0:
+            try:
+                heads.add((int(model_config.get_num_attention_heads(vllm_config.parallel_config)), hkv))
+            except (AttributeError, TypeError, ValueError):
+                pass
+        if (isinstance(max_seqs, int) and max_seqs > 0 and isinstance(max_tokens, int) and max_tokens > 0
+                and heads and torch.device(device).type == "cuda"):
+            Gfx906FAImpl.reserve_workspace(workspace_upper_bound(max_seqs, max_tokens, heads),
+                                           torch.device(device))
 
     def build_for_cudagraph_capture(self, common_attn_metadata: CommonAttentionMetadata
                                     ) -> Gfx906FAMetadata:
@@ -236,6 +246,14 @@ class Gfx906FAImpl(AttentionImpl):
     # shares its gather buffers the same way, lines 229-230).  Layers run in
     # order on one stream, so reuse is safe.
     _workspace: ClassVar[torch.Tensor | None] = None
+    # Workspaces replaced by a larger one.  A captured graph holds the raw
+    # address of the workspace it was captured with (the kernels receive
+    # pointers, so the graph keeps no reference to the tensor): a replaced
+    # workspace stays allocated for the life of the process, since later
+    # replays still write into it.
+    _retired: ClassVar[list[torch.Tensor]] = []
+    # (num_heads, num_kv_heads) of every layer built, for the workspace bound
+    _layer_heads: ClassVar[set[tuple[int, int]]] = set()
 
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
                  alibi_slopes: list[float] | None, sliding_window: int | None,
@@ -267,6 +285,7 @@ class Gfx906FAImpl(AttentionImpl):
         self.attn_type = attn_type
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
         self.num_queries_per_kv = num_heads // num_kv_heads
+        Gfx906FAImpl._layer_heads.add((num_heads, num_kv_heads))
 
     def fused_output_quant_supported(self, quant_key):
         return False
@@ -296,15 +315,21 @@ class Gfx906FAImpl(AttentionImpl):
 
     @classmethod
     def reserve_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor:
-        """Grow the shared workspace to at least nbytes (never shrinks)."""
+        """Grow the shared workspace to at least nbytes (never shrinks; grows
+        by at least a quarter, so few buffers are ever retired)."""
         ws = cls._workspace
         if ws is None or ws.numel() < nbytes or ws.device != device:
-            if torch.cuda.is_current_stream_capturing():
+            if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
                 raise RuntimeError(
                     f"GFX906_FA: attention workspace of {nbytes} bytes needed inside graph "
                     "capture; reserve it before capturing (Gfx906FAImpl.reserve_workspace)")
-            cls._workspace = None
-            cls._workspace = gfx906_fa.new_workspace(max(nbytes, 0 if ws is None else ws.numel()), device)
+            size = nbytes
+            if ws is not None and ws.device == device:
+                size = max(nbytes, ws.numel() + ws.numel() // 4)
+            new = gfx906_fa.new_workspace(size, device)
+            if ws is not None:
+                cls._retired.append(ws)
+            cls._workspace = new
         return cls._workspace
 
     @classmethod

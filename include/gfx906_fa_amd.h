@@ -206,6 +206,34 @@ size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int num_tokens
                                                     int head_size, int max_query_len,
                                                     int max_seq_len);
 
+/* (5-bound) Workspace bytes that cover every call of (5) / (5b) on the
+ *     current device with num_seqs <= max_num_seqs and num_tokens <=
+ *     max_num_tokens, whatever max_query_len and the mix of decode,
+ *     speculative-verify and prefill sequences: what a serving loop reserves
+ *     once, before graph capture, for a layer's (num_heads, num_kv_heads).
+ *     No reference counterpart (the reference grows its buffers per call,
+ *     extension/gfx906_fa_backend.py:316-403). */
+size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs, int64_t max_num_tokens,
+                                                     int num_heads, int num_kv_heads,
+                                                     int head_size);
+
+/* (5-info) The launch plan of a call shape, for tests and diagnostics:
+ *     info[0] workspace bytes, [1] decode classes, [2] largest decode row
+ *     bound, [3] prefill kernel launched, [4] prefill row tiles (bound),
+ *     [5] prefill work-list capacity, [6] split row tiles (bound), [7]
+ *     partial slots per kv-head, [8] byte offset in the workspace of the
+ *     prefill work-list header (int32 item count, int32 split row tile count,
+ *     written by the call; -1 without a work list), [9] CUs planned for.
+ *     Returns the number of entries (10; at most info_len are written), or
+ *     -1 for an invalid shape.  No reference counterpart. */
+int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tokens, int num_heads,
+                                            int num_kv_heads, int head_size, int max_query_len,
+                                            int max_seq_len, int64_t *info, int info_len);
+
+/* Compute units of the current device the plans are made for (256, the
+ * MI355X count, when no device is visible).  No reference counterpart. */
+int gfx906_fa_amd_device_cus(void);
+
 hipError_t gfx906_fa_amd_paged_attention(
     const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
     const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,

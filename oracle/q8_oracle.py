@@ -32,7 +32,9 @@ Pinning (what checks each function beyond restating it):
   ``kernel/fattn-q8.cuh:646-653``, GQA map of ``kernel/fattn-q8.cuh:898-901``.
   Pinned by: torch SDPA (math backend, float64) on the same dequantized
   inputs, a single visible key giving the V row, uniform scores giving the
-  mean of V, invariance to block_table permutation.
+  mean of V, invariance to block_table permutation.  Its per-kv-head core
+  ``attention_rows_ref`` (explicit per-row key bounds, used directly by the
+  GPU tests' sampled-row checks) is pinned through it by the same checks.
 * ``flat_attention_ref`` - the contiguous path of the op module's
   ``forward`` (``extension/gfx906_fa.cpp:120-265``): dequantized K, exact
   fp16 V, kv_max cutoff and inline causal bound.  Pinned by: torch SDPA
@@ -153,8 +155,8 @@ def quantize_q8_0_rows(x) -> np.ndarray:
 def dequantize_blocks(q: np.ndarray, d: np.ndarray) -> np.ndarray:
     """x_hat = float(fp16 d) * float(int8 q)  (``tests/test_q8_roundtrip.py:21-36``)."""
     D = q.shape[-1]
-    dd = np.repeat(d.astype(np.float32), QK8_0, axis=-1)
-    return (q.astype(np.float32) * dd).astype(np.float32).reshape(q.shape[:-1] + (D,))
+    qb = q.astype(np.float32).reshape(q.shape[:-1] + (D // QK8_0, QK8_0))
+    return (qb * d.astype(np.float32)[..., None]).astype(np.float32).reshape(q.shape[:-1] + (D,))
 
 
 def dequantize_q8_0_rows(rows: np.ndarray, D: int) -> np.ndarray:
@@ -323,29 +325,33 @@ def planar_cache_write(key, value, slot_mapping: np.ndarray, cache: np.ndarray) 
 
 
 def planar_to_aos(cache: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Planar cache -> (K AoS [NB, bs, Hkv, 136], V AoS [NB, bs, Hkv, 136])."""
+    """Planar cache -> (K AoS [NB, bs, Hkv, 136], V AoS [NB, bs, Hkv, 136]).
+
+    The position maps above are products of index splits, so a sub-page
+    unpacks by reshape + transpose:
+      K ints  [b//2][t][g][b%2][d%8] -> [t][b][g][d%8]    (d = 32b + 8g + d%8)
+      K scales [t][b]
+      V ints  [m//4][t//4][d%16][m%4][t%4] -> [t//4][t%4][m][d%16]  (d = 16m + d%16)
+      V scales [t//4][b][t%4] -> [t//4][t%4][b]"""
     NB, _, Hkv, nbytes = cache.shape
-    bs = (nbytes // SUBPAGE_BYTES) * PAGE_TOKENS
-    ko = np.zeros((NB, bs, Hkv, 136), dtype=np.uint8)
-    vo = np.zeros((NB, bs, Hkv, 136), dtype=np.uint8)
-    tt = np.arange(bs)
-    sp, t16 = tt // PAGE_TOKENS, tt % PAGE_TOKENS
-    dd = np.arange(128)
-    # vectorised gather of all rows
-    kidx = (sp * SUBPAGE_BYTES)[:, None] + planar_kpos(t16[:, None], dd[None, :])
-    vidx = (sp * SUBPAGE_BYTES)[:, None] + planar_vpos(t16[:, None], dd[None, :])
-    bb = np.arange(8) // 2
-    for plane, out, idx in ((0, ko, kidx), (1, vo, vidx)):
-        sidx = (sp * SUBPAGE_BYTES)[:, None] + planar_spos(plane, t16[:, None], bb[None, :]) + np.arange(8)[None, :] % 2
-        buf = cache[:, plane]                      # [NB, Hkv, nbytes]
-        q = buf[:, :, idx]                         # [NB, Hkv, bs, 128]
-        s = buf[:, :, sidx]                        # [NB, Hkv, bs, 8]
-        q = np.transpose(q, (0, 2, 1, 3))
-        s = np.transpose(s, (0, 2, 1, 3))
-        o = out.reshape(NB, bs, Hkv, 4, 34)
-        o[..., :2] = s.reshape(NB, bs, Hkv, 4, 2)
-        o[..., 2:] = q.reshape(NB, bs, Hkv, 4, 32)
-    return ko, vo
+    nsp = nbytes // SUBPAGE_BYTES
+    bs = nsp * PAGE_TOKENS
+    sub = np.ascontiguousarray(cache).reshape(NB, 2, Hkv, nsp, SUBPAGE_BYTES)
+    ints, scales = sub[..., :2048], sub[..., 2048:]
+    lead = (NB, Hkv, nsp)
+    kq = ints[:, 0].reshape(*lead, 2, 16, 4, 2, 8).transpose(0, 1, 2, 4, 3, 6, 5, 7)  # t, bh, bl, g, e
+    kq = kq.reshape(*lead, 16, 4, 32)
+    ks = scales[:, 0].reshape(*lead, 16, 4, 2)
+    vq = ints[:, 1].reshape(*lead, 2, 4, 16, 4, 4).transpose(0, 1, 2, 4, 7, 3, 6, 5)  # tq, tl, mh, ml, dl
+    vq = vq.reshape(*lead, 16, 4, 32)
+    vs = scales[:, 1][..., :128].reshape(*lead, 4, 4, 4, 2).transpose(0, 1, 2, 3, 5, 4, 6)  # tq, tl, b
+    vs = vs.reshape(*lead, 16, 4, 2)
+    out = []
+    for q, sc in ((kq, ks), (vq, vs)):
+        rows = np.concatenate([sc, q], axis=-1)                  # [NB, Hkv, nsp, 16, 4, 34]
+        rows = rows.reshape(NB, Hkv, bs, 136).transpose(0, 2, 1, 3)
+        out.append(np.ascontiguousarray(rows))
+    return out[0], out[1]
 
 
 def planar_dequant(cache: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
@@ -357,6 +363,31 @@ def planar_dequant(cache: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 # ---------------------------------------------------------------------------
 # Attention reference
 # ---------------------------------------------------------------------------
+def attention_rows_ref(q: np.ndarray, K: np.ndarray, V: np.ndarray, lim: np.ndarray,
+                       scale: float) -> np.ndarray:
+    """The softmax core of ``paged_attention_ref`` for the query heads of one
+    kv-head: q [n, G, D] (n query rows of G heads each), K / V [L, D] that
+    kv-head's dequantized keys and values in position order, lim [n]: row i
+    sees keys k <= lim[i].  -> float64 [n, G, D]; a row with no visible key
+    (lim < 0) outputs 0."""
+    q = np.asarray(q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    lim = np.asarray(lim, np.int64)
+    pos = np.arange(K.shape[0])
+    mask = pos[None, :] <= lim[:, None]              # [n, L]
+    n, G, D = q.shape
+    sc = (q.reshape(n * G, D) @ K.T).reshape(n, G, -1) * scale
+    sc = np.where(mask[:, None, :], sc, -np.inf)
+    m = np.max(sc, axis=-1, keepdims=True) if sc.shape[-1] else np.zeros(sc.shape[:-1] + (1,))
+    m = np.where(np.isfinite(m), m, 0.0)
+    p = np.exp(sc - m)
+    p = np.where(mask[:, None, :], p, 0.0)
+    l = p.sum(-1, keepdims=True)
+    o = (p.reshape(n * G, -1) @ V).reshape(n, G, V.shape[1])
+    return np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
+
+
 def paged_attention_ref(query: np.ndarray, k_hat: np.ndarray, v_hat: np.ndarray,
                         block_table: np.ndarray, seq_lens: np.ndarray,
                         query_start_loc: np.ndarray, scale: float) -> np.ndarray:
@@ -382,23 +413,12 @@ def paged_attention_ref(query: np.ndarray, k_hat: np.ndarray, v_hat: np.ndarray,
             continue
         pos = np.arange(sl)
         pages = block_table[s, pos // bs].astype(np.int64)
-        K = k_hat[pages, pos % bs].astype(np.float64)   # [sl, Hkv, D]
-        V = v_hat[pages, pos % bs].astype(np.float64)
-        qs = query[q0:q1].astype(np.float64)             # [nq, Hq, D]
+        K = k_hat[pages, pos % bs]                       # [sl, Hkv, D]
+        V = v_hat[pages, pos % bs]
         lim = sl - nq + np.arange(nq)                    # [nq]
-        mask = pos[None, :] <= lim[:, None]              # [nq, sl]
         for h in range(Hkv):
-            qh = qs[:, h * G:(h + 1) * G, :]             # [nq, G, D]
-            sc = np.einsum("ngd,kd->ngk", qh, K[:, h, :]) * scale
-            sc = np.where(mask[:, None, :], sc, -np.inf)
-            m = np.max(sc, axis=-1, keepdims=True)
-            m = np.where(np.isfinite(m), m, 0.0)
-            p = np.exp(sc - m)
-            p = np.where(mask[:, None, :], p, 0.0)
-            l = p.sum(-1, keepdims=True)
-            o = np.einsum("ngk,kd->ngd", p, V[:, h, :])
-            o = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
-            out[q0:q1, h * G:(h + 1) * G, :] = o
+            out[q0:q1, h * G:(h + 1) * G, :] = attention_rows_ref(
+                query[q0:q1, h * G:(h + 1) * G, :], K[:, h, :], V[:, h, :], lim, scale)
     return out
 
 

@@ -70,40 +70,42 @@ def stream_ptr():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def batch_oracle(b, rows=None):
+def seq_head_kv(b, s, h):
+    """Dequantized K, V float32 [seq_len, 128] of sequence s, kv-head h, read
+    from the GPU-written planar cache (whose bytes are checked separately):
+    only that sequence's pages and that head's planes are copied."""
+    sl = int(b.seq_lens[s])
+    bs = b.block_size
+    npg = max((sl + bs - 1) // bs, 1)
+    pages = torch.from_numpy(b.block_table_np[s, :npg].astype(np.int64)).to(b.kv_cache.device)
+    sub = b.kv_cache.index_select(0, pages)[:, :, h:h + 1].cpu().numpy()
+    kh, vh = O.planar_dequant(np.ascontiguousarray(sub))
+    return kh.reshape(npg * bs, 128)[:sl], vh.reshape(npg * bs, 128)[:sl]
+
+
+def batch_oracle(b, rows=None, q_abs=None, causal=True):
     """float64 oracle output [T, Hq, D] for a workloads.Batch, computed from
-    the GPU-written planar cache (whose bytes are checked separately), only
-    over the pages the batch references.  rows: optional list of query
-    token indices to restrict the work (others left 0)."""
-    bt = b.block_table_np
+    the GPU-written planar cache, one (sequence, kv-head) at a time.
+    rows: optional list of query token indices to restrict the work (the
+    others are left 0).  Row j of sequence s sees keys k < seq_len with
+    k <= q_abs[s] + j when causal (q_abs defaults to seq_len - n_q)."""
     q = to_np_f32(b.query)
     qsl = b.qsl
-
-    def pages_of(seqs):
-        """Dequantized sub-cache holding only the pages of `seqs`, and the
-        remapped block table."""
-        sel = bt[seqs]
-        used = np.unique(sel[sel >= 0])
-        idx = torch.from_numpy(used).to(b.kv_cache.device)
-        sub = b.kv_cache.index_select(0, idx).cpu().numpy()
-        remap = np.full(b.num_blocks, -1, np.int64)
-        remap[used] = np.arange(len(used))
-        kh, vh = O.planar_dequant(sub)
-        return kh, vh, np.where(sel >= 0, remap[np.maximum(sel, 0)], -1).astype(np.int32)
-
-    if rows is None:
-        kh, vh, bt2 = pages_of(np.arange(b.num_seqs))
-        return O.paged_attention_ref(q, kh, vh, bt2, b.seq_lens, qsl, b.scale)
+    G = b.Hq // b.Hkv
     out = np.zeros(q.shape, np.float64)
-    for tkn in rows:
-        s = int(np.searchsorted(qsl, tkn, side="right") - 1)
-        j = tkn - int(qsl[s])
-        nq = int(qsl[s + 1] - qsl[s])
+    toks = np.arange(b.num_tokens) if rows is None else np.asarray(sorted(set(int(r) for r in rows)))
+    seq_of = np.searchsorted(qsl, toks, side="right") - 1
+    for s in np.unique(seq_of):
+        s = int(s)
+        ts = toks[seq_of == s]
         sl = int(b.seq_lens[s])
-        kh, vh, bt2 = pages_of(np.array([s]))
-        # one-row sequence ending at the row's causal limit
-        lim = sl - nq + j + 1
-        o = O.paged_attention_ref(q[tkn:tkn + 1], kh, vh, bt2, np.array([lim], np.int32),
-                                  np.array([0, 1], np.int32), b.scale)
-        out[tkn] = o[0]
+        nq = int(qsl[s + 1] - qsl[s])
+        if sl <= 0:
+            continue
+        j = ts - int(qsl[s])
+        qa = sl - nq if q_abs is None else int(q_abs[s])
+        lim = np.minimum(qa + j, sl - 1) if causal else np.full(len(ts), sl - 1)
+        for h in range(b.Hkv):
+            K, V = seq_head_kv(b, s, h)
+            out[ts, h * G:(h + 1) * G] = O.attention_rows_ref(q[ts, h * G:(h + 1) * G], K, V, lim, b.scale)
     return out

@@ -138,18 +138,86 @@ def test_q8_0_pages_hold_exactly_the_planes(bs):
 
 def test_graph_support_and_workspace_bound():
     """The builder declares graph support for uniform batches; the workspace
-    it reserves up front covers every batch of up to max_num_seqs sequences,
-    whatever the heads, query length or context."""
+    bound covers every batch of up to max_num_seqs sequences and
+    max_num_tokens tokens: uniform and non-uniform query lengths (both decode
+    classes plus prefill rows in one batch), chunked-prefill token budgets,
+    and kv-head counts that do not divide the CU count."""
+    import random
     import gfx906_fa
     from gfx906_fa_backend import Gfx906FAMetadataBuilder, workspace_upper_bound
     from vllm.v1.attention.backend import AttentionCGSupport
     assert Gfx906FAMetadataBuilder._cudagraph_support == AttentionCGSupport.UNIFORM_BATCH
-    for max_seqs in (1, 7, 256):
-        bound = workspace_upper_bound(max_seqs)
-        for n in {1, max_seqs // 2 or 1, max_seqs}:
-            for Hq, Hkv in ((48, 8), (6, 1), (32, 32)):
-                for mq in (1, 4, 5, 16, 2048):
-                    assert gfx906_fa.workspace_size(n, n * mq, Hq, Hkv, mq, 1 << 17) <= bound
+    rng = random.Random(0)
+    heads = ((48, 8), (6, 1), (32, 32), (12, 3), (10, 5), (36, 6), (40, 10), (48, 12), (64, 1), (128, 1),
+             (8, 1), (96, 3))
+    for hq, hkv in heads:
+        for max_seqs, max_tokens in ((1, 1), (1, 8192), (7, 7), (7, 4096), (256, 256), (256, 8192),
+                                     (256, 65536), (1024, 16384)):
+            bound = workspace_upper_bound(max_seqs, max_tokens, [(hq, hkv)])
+            assert bound == gfx906_fa.workspace_bound(max_seqs, max_tokens, hq, hkv) > 0
+            shapes = []
+            for n in {1, max(1, max_seqs // 2), max_seqs}:
+                for mq in (1, 2, 5, 6, 16, 2048):
+                    if n * mq <= max_tokens:
+                        shapes.append((n, n * mq, mq))          # uniform
+                        if n > 1:
+                            shapes.append((n, n * mq - 1, mq))  # one sequence a token short
+                if n <= max_tokens:
+                    # one long prefill chunk with n - 1 decode / verify sequences
+                    for extra in (1, 5, 6):
+                        big = max_tokens - extra * (n - 1)
+                        if big >= 1:
+                            shapes.append((n, big + extra * (n - 1), big))
+            for _ in range(40):
+                n = rng.randint(1, max_seqs)
+                if n > max_tokens:
+                    continue
+                T = rng.randint(n, max_tokens)
+                shapes.append((n, T, rng.randint(1, T - n + 1)))
+            for n, T, mq in shapes:
+                need = gfx906_fa.workspace_size(n, T, hq, hkv, mq, 1 << 17)
+                assert need <= bound, (hq, hkv, max_seqs, max_tokens, n, T, mq, need, bound)
+    # several layer shapes: the largest bound
+    both = workspace_upper_bound(64, 4096, [(48, 8), (6, 1)])
+    assert both == max(gfx906_fa.workspace_bound(64, 4096, 48, 8), gfx906_fa.workspace_bound(64, 4096, 6, 1))
+
+
+def test_builder_reserves_the_bound_and_retires_workspaces(monkeypatch):
+    """The builder reserves the bound for the scheduler limits and the layer
+    shapes; a larger request later replaces the workspace but keeps the old
+    one alive (a captured graph may still write into it)."""
+    import types
+    import gfx906_fa
+    import gfx906_fa_backend as GB
+    from gfx906_fa_backend import Gfx906FAImpl, Gfx906FAMetadataBuilder, workspace_upper_bound
+    from vllm.v1.kv_cache_interface import AttentionSpec
+    made = []
+
+    def fake_new_workspace(nbytes, device):
+        t = torch.empty(max(int(nbytes), 256), dtype=torch.uint8)
+        made.append(t)
+        return t
+
+    monkeypatch.setattr(gfx906_fa, "new_workspace", fake_new_workspace)
+    monkeypatch.setattr(Gfx906FAImpl, "_workspace", None)
+    monkeypatch.setattr(Gfx906FAImpl, "_retired", [])
+    monkeypatch.setattr(Gfx906FAImpl, "_layer_heads", set())
+    Gfx906FAImpl(48, 128, 0.1, 8, None, None, "auto")
+    Gfx906FAImpl(6, 128, 0.1, 1, None, None, "auto")
+    cfg = types.SimpleNamespace(scheduler_config=types.SimpleNamespace(max_num_seqs=128,
+                                                                       max_num_batched_tokens=8192))
+    # a CPU device never reserves (no GPU here): the bound is reserved for cuda only
+    Gfx906FAMetadataBuilder(AttentionSpec(block_size=16, num_kv_heads=8), ["l0"], cfg, torch.device("cpu"))
+    assert Gfx906FAImpl._workspace is None
+    want = workspace_upper_bound(128, 8192, [(48, 8), (6, 1)])
+    cpu = torch.device("cpu")
+    first = Gfx906FAImpl.reserve_workspace(want, cpu)
+    assert first.numel() >= want and Gfx906FAImpl._retired == []
+    assert Gfx906FAImpl.reserve_workspace(want // 2, cpu) is first      # never shrinks
+    second = Gfx906FAImpl.reserve_workspace(want + 1, cpu)
+    assert second is not first and second.numel() >= want + want // 4  # grows by a quarter at least
+    assert Gfx906FAImpl._retired == [first]                              # the old one stays alive
+    assert GB.Gfx906FAImpl._workspace is second
 
 
 def test_forward_debug_log_records_the_call_and_its_failure(tmp_path, monkeypatch):

@@ -23,7 +23,9 @@ def test_header_declares_expected_entry_points():
     for n in ["launch_quantize_q8_0_dense", "launch_reshape_and_cache_q8",
               "launch_gather_paged_kv_q8", "gfx906_fa_amd_cache_write_kv",
               "gfx906_fa_amd_paged_attention", "gfx906_fa_amd_paged_attention_workspace_size",
-              "gfx906_fa_amd_gather_planar", "gfx906_fa_amd_gather_rows"]:
+              "gfx906_fa_amd_gather_planar", "gfx906_fa_amd_gather_rows",
+              "gfx906_fa_amd_paged_attention_workspace_bound", "gfx906_fa_amd_paged_attention_plan_info",
+              "gfx906_fa_amd_device_cus"]:
         assert n in names
 
 
@@ -93,14 +95,38 @@ def test_workspace_size_plan():
     # independent of the context length (stream-K shares work per wave)
     assert gfx906_fa.workspace_size(32, 32, 48, 8, 1, 1 << 20) == b
     # a prefill launch also holds the partials of split row tiles: 3 ceil(CUs / Hkv)
-    # slots per kv head of 256 rows x (128 + 2) floats (256 CUs without a GPU)
+    # slots per kv head of 256 rows x (128 + 2) floats.  The CU count is the
+    # library's own query (the device's count on a GPU host; without a device
+    # the library plans for 256, the MI355X count, which this then pins)
+    cus = gfx906_fa.device_cus()
+    assert cus > 0
     pf = gfx906_fa.workspace_size(1, 50, 48, 8, 50, 65586)
-    assert pf >= 3 * 32 * 8 * 256 * 130 * 4
+    assert pf >= 3 * (-(-cus // 8)) * 8 * 256 * 130 * 4
     assert gfx906_fa.workspace_size(1, 50, 48, 8, 50, 1 << 20) == pf
     # kv-head counts that do not divide the CU count round the slots up per head
     for hkv in (3, 5, 7, 12):
-        need = 3 * (-(-256 // hkv)) * hkv * 256 * 130 * 4
+        need = 3 * (-(-cus // hkv)) * hkv * 256 * 130 * 4
         assert gfx906_fa.workspace_size(2, 200, 2 * hkv, hkv, 100, 9000) >= need
+        info = gfx906_fa.plan_info(2, 200, 2 * hkv, hkv, 100, 9000)
+        assert info["pf_slots_max"] == 3 * (-(-cus // hkv)) and info["cus"] == cus
+        assert info["bytes"] == gfx906_fa.workspace_size(2, 200, 2 * hkv, hkv, 100, 9000)
+
+
+def test_plan_info():
+    import torch
+    import gfx906_fa
+    if not torch.cuda.is_available():
+        assert gfx906_fa.device_cus() == 256  # the fallback without a device
+    d = gfx906_fa.plan_info(32, 32, 48, 8, 1, 16384)   # cfg2 decode: one class, no prefill
+    assert (d["decode_classes"], d["dec_rows_max"], d["prefill"], d["pf_header_offset"]) == (1, 16, 0, -1)
+    v = gfx906_fa.plan_info(8, 40, 6, 1, 5, 131077)    # 30 verify rows: the 32-row class
+    assert (v["decode_classes"], v["dec_rows_max"], v["prefill"]) == (1, 32, 0)
+    m = gfx906_fa.plan_info(64, 8252, 48, 8, 2048, 131072)  # mixed: both classes and a work list
+    assert (m["decode_classes"], m["dec_rows_max"], m["prefill"]) == (2, 64, 1)
+    assert 0 < m["pf_header_offset"] < m["bytes"] and m["pf_header_offset"] % 256 == 0
+    assert gfx906_fa.plan_info(1, 32768, 48, 8, 32768, 32768)["decode_classes"] == 0
+    with pytest.raises(RuntimeError):
+        gfx906_fa.plan_info(1, 1, 6, 4, 1, 1)             # heads not divisible
 
 
 def test_ops_reject_cpu_tensors():

@@ -345,34 +345,103 @@ def _permuted_copy(b, seed=99):
     return cache2, bt2
 
 
-@pytest.mark.parametrize("name", ["cfg2", "cfg5"])
-def test_full_size_decode_configs(name):
-    need_gpu()
-    b = W.build_cfg(name, device=DEV)
-    sample = sorted(set(np.linspace(0, b.num_tokens - 1, 6).astype(int).tolist()))
-    out = _run_and_check(b, rows=sample)
+def _check_permutation_invariance(b, out, name):
     announce(f"{name} permutation invariance")
     cache2, bt2 = _permuted_copy(b)
     out2 = gfx906_fa.paged_attention(b.query, cache2[:, 0], cache2[:, 1], bt2, b.seq_lens_t, b.qsl_t,
                                      b.max_query_len, b.max_seq_len, b.scale, out_dtype=out.dtype)
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
+    del cache2
+
+
+@pytest.mark.parametrize("name", ["cfg2", "cfg5"])
+def test_full_size_decode_configs(name):
+    """cfg2 (32 decode tokens) and cfg5 at 6/1 (8 x 5 verify tokens): every
+    query token, every head, against the oracle."""
+    need_gpu()
+    b = W.build_cfg(name, device=DEV)
+    out = _run_and_check(b, rows=list(range(b.num_tokens)))
+    _check_permutation_invariance(b, out, name)
+
+
+def test_full_size_verify_cfg5_48_8():
+    """cfg5 rerun at the full 48/8 head shape: 8 x (131072 + 5) cached tokens,
+    2.28 GB of Q8 K+V, 5 tokens x 6 q-heads = 30 packed rows per sequence and
+    kv-head (the two-row-group decode class).  Every verify token of three
+    sequences (first, middle, last), all 48 heads - so all 8 kv-heads -
+    against the oracle; the whole output is invariant under a page
+    permutation.  Shape: the reference's TP-8 deployment
+    (tests/test_fa_mixed_batch.py:36-37) unsharded, verifying 1 + 4 n-gram
+    draft tokens (scripts/start_vllm_fa_ngram.sh:35-39)."""
+    need_gpu()
+    b = W.build_cfg("cfg5", device=DEV, heads=(48, 8))
+    qsl = b.qsl
+    rows = [t for s in (0, 3, 7) for t in range(int(qsl[s]), int(qsl[s + 1]))]
+    out = _run_and_check(b, rows=rows)
+    _check_permutation_invariance(b, out, "cfg5 48/8")
 
 
 def test_full_size_prefill_cfg3():
+    """cfg3, 32K causal prefill at 48/8: one query token per 8 row tiles of
+    256 packed rows (every 341st token), the first and last tokens and the
+    sub-page edges, every head."""
     need_gpu()
     b = W.build_cfg("cfg3", device=DEV)
     T = b.num_tokens
-    sample = [0, 1, 15, 16, 17, 1000, 4097, T // 2, T - 2, T - 1]
+    rng = np.random.default_rng(3)
+    sample = sorted(set(range(0, T, 341)) | {0, 1, 15, 16, 17, 63, 64, 4097, T // 2, T - 2, T - 1}
+                    | set(rng.integers(0, T, 8).tolist()))
     _run_and_check(b, out_dtype=torch.float32, rows=sample)
 
 
 def test_full_size_mixed_cfg4():
+    """cfg4: twelve tokens of each 2048-token chunk (first and last
+    included) and every fourth of the 60 decode sequences, every head."""
     need_gpu()
     b = W.build_cfg("cfg4", device=DEV)
     qsl = b.qsl
-    sample = [0, 2047, 2048 + 5, 3 * 2048 + 2047] + [int(qsl[4 + i]) for i in (0, 17, 59)]
-    _run_and_check(b, rows=sample)
+    sample = []
+    for c in range(4):
+        sample += np.linspace(int(qsl[c]), int(qsl[c + 1]) - 1, 12).astype(int).tolist()
+    sample += [int(qsl[4 + i]) for i in range(0, 60, 4)] + [int(qsl[63])]
+    _run_and_check(b, rows=sorted(set(sample)))
+
+
+def test_seed_sweep_error_margin():
+    """20 seeds of N(0,1) inputs: short causal prefills (fp16 and bf16, GQA
+    4:1 and 6:1, a first row that sees one key) and decode batches, each
+    whole output against the oracle at the north-star tolerance (max-abs
+    2e-3 for fp32 output).  The worst max-abs error over the sweep is
+    written to $GFA_SEED_SWEEP_OUT (JSON) when that is set."""
+    need_gpu()
+    worst = {}
+    for seed in range(20):
+        rng = np.random.default_rng(500 + seed)
+        dt = "bf16" if seed % 2 else "f16"
+        hq, hkv = ((8, 2), (48, 8), (6, 1), (32, 8))[seed % 4]
+        L = int(rng.integers(150, 700))
+        cases = {
+            "prefill": W.build_batch([L], [L], hq, hkv, dtype=dt, seed=600 + seed),
+            "chunk": W.build_batch([L + 300, 40], [L, 40], hq, hkv, dtype=dt, seed=700 + seed),
+            "decode": W.build_batch(rng.integers(1, 3000, 8).tolist(), [1] * 8, hq, hkv, dtype=dt,
+                                    seed=800 + seed),
+        }
+        for kind, b in cases.items():
+            announce(f"seed sweep {seed} {kind} {dt} {hq}/{hkv}")
+            out = W.attention(b, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            ref = batch_oracle(b)
+            got = to_np_f32(out)
+            err = float(np.abs(got - ref).max())
+            if err > worst.get(kind, (0.0,))[0]:
+                worst[kind] = (err, seed, dt, f"{hq}/{hkv}")
+            assert_close(got, ref)
+    if os.environ.get("GFA_SEED_SWEEP_OUT"):
+        import json
+        with open(os.environ["GFA_SEED_SWEEP_OUT"], "w") as f:
+            json.dump({k: {"max_abs": v[0], "seed": v[1], "dtype": v[2], "heads": v[3]}
+                       for k, v in worst.items()}, f, indent=1)
 
 
 def test_decode_many_short_sequences():

@@ -32,7 +32,23 @@ CASES = [
     ("gqa4_chunk200_ctx12k", [12000 + 200], [200], 32, 8),
     ("mqa_fresh2048", [2048], [2048], 8, 1),                 # causal from key 0, 64 row tiles
     ("two_rounds_16x100_ctx4k", [4096 + 100] * 16, [100] * 16, 48, 8),  # 48 row tiles: cut for 3 rounds
+    # more than 1024 row tiles (the plan's per-item key-tile counts are then
+    # recomputed instead of kept in LDS, and a capacity check runs): a fresh
+    # 33000-token prefill (1032 row tiles at 8 rows per token) with a 40-token
+    # chunk on a 100000-token context whose two row tiles exceed one CU's
+    # share of the launch's key tiles and are cut
+    ("many_tiles_33000_plus_chunk40_ctx100k", [33000, 100000 + 40], [33000, 40], 8, 1),
 ]
+
+
+def _split_header(ws, b):
+    """(work items, row tiles split over the keys) the call's plan kernel left
+    in the workspace."""
+    info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
+    off = info["pf_header_offset"]
+    assert off >= 0, "the call has no prefill work list"
+    hdr = ws[off:off + 8].view(torch.int32).cpu().tolist()
+    return hdr[0], hdr[1]
 
 
 def _sample(b, n=48, seed=0):
@@ -52,8 +68,17 @@ def test_split_prefill_matches_oracle(case):
     name, sls, qls, Hq, Hkv = case
     announce(f"prefill split {name}")
     b = W.build_batch(sls, qls, Hq, Hkv, seed=sum(map(ord, name)))
-    out = W.attention(b, out_dtype=torch.float32)
+    ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(b.num_seqs, b.num_tokens, Hq, Hkv, b.max_query_len,
+                                                          b.max_seq_len), DEV)
+    out = W.attention(b, out_dtype=torch.float32, workspace=ws)
     torch.cuda.synchronize()
+    items, nsplit = _split_header(ws, b)
+    dec_max = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, Hq, Hkv, b.max_query_len, b.max_seq_len)["dec_rows_max"]
+    tiles = sum(-(-q * (Hq // Hkv) // 256) for q in qls if q * (Hq // Hkv) > dec_max)
+    # the plan split something: pieces beyond the row tiles, split row tiles listed
+    assert nsplit > 0 and items > tiles, (items, nsplit, tiles)
+    if name.startswith("many_tiles"):
+        assert tiles > 1024
     rows = _sample(b) if b.num_tokens > 400 else None
     ref = batch_oracle(b, rows=rows)
     got = to_np_f32(out)

@@ -252,3 +252,84 @@ def test_roundtrip_write_gather_dequant():
         rec = O.dequantize_q8_0_rows(got[0].permute(1, 0, 2).cpu().numpy(), 128)
         ref = O.dequantize_q8_0_rows(gfx906_fa.quantize_q8_0(src).cpu().numpy(), 128)
         assert np.array_equal(rec, ref)
+
+
+def _ref_abi():
+    """This library's reference-named launchers, with their reference
+    signatures (extension/gfx906_fa.cpp:38-115)."""
+    return gfx906_fa.lib()
+
+
+def test_reference_named_quantize_and_cache_write():
+    """launch_quantize_q8_0_dense and launch_reshape_and_cache_q8 of THIS
+    library, called as the reference's binding calls them
+    (extension/gfx906_fa.cpp:273-374): fp16 input, key strides in elements,
+    cache strides in bytes, slot < 0 skipped - byte for byte against the
+    oracle."""
+    need_gpu()
+    L = _ref_abi()
+    announce("reference ABI: launch_quantize_q8_0_dense")
+    x = _rand((777, 128), "f16", 1.0, seed=40)
+    x[:100] *= 1e-3
+    y = torch.full((777, 136), 0xCD, dtype=torch.uint8, device=DEV)
+    assert L.launch_quantize_q8_0_dense(x.data_ptr(), y.data_ptr(), 777, 128, stream_ptr()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), O.quantize_q8_0_rows(host_bits(x)))
+    x64 = _rand((33, 64), "f16", 3.0, seed=41)   # D = 64: two blocks per row
+    y64 = torch.empty((33, 68), dtype=torch.uint8, device=DEV)
+    assert L.launch_quantize_q8_0_dense(x64.data_ptr(), y64.data_ptr(), 33, 64, stream_ptr()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(y64.cpu().numpy(), O.quantize_q8_0_rows(host_bits(x64)))
+
+    announce("reference ABI: launch_reshape_and_cache_q8")
+    NB, bs, Hkv, D, T = 7, 16, 4, 128, 50
+    fused = _rand((T, 3, Hkv, D), "f16", 1.0, seed=42)
+    key = fused[:, 1]                                   # token stride 3*Hkv*D elements
+    rng = np.random.default_rng(43)
+    slots = rng.permutation(NB * bs)[:T].astype(np.int64)
+    slots[[3, 17]] = -1
+    sl_t = torch.from_numpy(slots).to(DEV)
+    cache = torch.full((NB, bs, Hkv, 136), 0x5A, dtype=torch.uint8, device=DEV)
+    err = L.launch_reshape_and_cache_q8(key.data_ptr(), sl_t.data_ptr(), cache.data_ptr(), T, Hkv, D, bs,
+                                        key.stride(0), key.stride(1), cache.stride(0), cache.stride(1),
+                                        cache.stride(2), stream_ptr())
+    assert err == 0
+    torch.cuda.synchronize()
+    exp = np.full((NB, bs, Hkv, 136), 0x5A, np.uint8)
+    O.reshape_and_cache_q8_aos(host_bits(key.contiguous()), slots, exp)
+    assert np.array_equal(cache.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("v_row_elems", [128, 160, 130])
+def test_reference_named_gather(v_row_elems):
+    """launch_gather_paged_kv_q8 of THIS library with the reference's
+    conventions (extension/gfx906_fa_gather.cu:362-425): K cache strides in
+    bytes, V cache strides in fp16 elements (converted to bytes inside).  V
+    rows padded to 160 or 130 elements make the element strides differ from
+    the byte strides (130 also leaves rows only 4-byte aligned).  Against
+    the oracle's v2 contract: V zeroed and K untouched on invalid tokens,
+    -1 pages, seq_len 0, Sk past the table."""
+    need_gpu()
+    L = _ref_abi()
+    announce(f"reference ABI: launch_gather_paged_kv_q8 v_row={v_row_elems}")
+    rng = np.random.default_rng(44)
+    NB, bs, Hkv, D, B, M = 40, 16, 3, 128, 5, 6
+    kc = torch.from_numpy(rng.integers(0, 256, (NB, bs, Hkv, 136), dtype=np.uint8)).to(DEV)
+    vfull = torch.from_numpy(rng.standard_normal((NB, bs, Hkv, v_row_elems)).astype(np.float16)).to(DEV)
+    vc = vfull[..., :D]
+    bt = rng.integers(0, NB, (B, M)).astype(np.int32)
+    bt[1, 4] = -1
+    sl = np.array([0, 90, 17, M * bs, 33], np.int32)
+    Sk = ((M * bs + 20 + 31) // 32) * 32               # past the table
+    btt, slt = torch.from_numpy(bt).to(DEV), torch.from_numpy(sl).to(DEV)
+    ko = torch.full((B, Hkv, Sk, 136), 0xAB, dtype=torch.uint8, device=DEV)
+    vo = torch.full((B, Hkv, Sk, D), 7.0, dtype=torch.float16, device=DEV)
+    err = L.launch_gather_paged_kv_q8(kc.data_ptr(), vc.data_ptr(), btt.data_ptr(), slt.data_ptr(), ko.data_ptr(),
+                                      vo.data_ptr(), B, Hkv, Sk, D, 136, bs, M, kc.stride(0), kc.stride(1),
+                                      kc.stride(2), vc.stride(0), vc.stride(1), vc.stride(2), stream_ptr())
+    assert err == 0
+    torch.cuda.synchronize()
+    ke, ve = O.gather_paged_kv_q8_aos(kc.cpu().numpy(), vc.contiguous().cpu().numpy(), bt, sl, Sk,
+                                      k_out=np.full((B, Hkv, Sk, 136), 0xAB, np.uint8))
+    assert np.array_equal(ko.cpu().numpy(), ke)
+    assert np.array_equal(vo.cpu().numpy(), ve)

@@ -220,6 +220,36 @@ def test_cpu_baseline_matches_oracle():
     assert nseq >= 1 and tokens >= 40 and secs > 0
 
 
+def test_cpu_prefill_baseline_matches_oracle():
+    """The timed q-chunked CPU prefill (one kv-head's query heads, chunks of
+    the prompt in spread order) computes the oracle's causal attention for
+    those heads; the thread count is the process's CPU share."""
+    import os
+    from oracle import cpu_baseline as CB
+    rng = np.random.default_rng(9)
+    bs, Hkv, Hq, L = 16, 2, 6, 150
+    bt, nb = O.make_block_table(rng, [L], bs)
+    cache = np.zeros(O.planar_cache_shape(nb, bs, Hkv), np.uint8)
+    k = rng.standard_normal((nb * bs, Hkv, 128)).astype(np.float16)
+    v = rng.standard_normal((nb * bs, Hkv, 128)).astype(np.float16)
+    O.planar_cache_write(k, v, np.arange(nb * bs, dtype=np.int64), cache)
+    q = rng.standard_normal((L, Hq, 128)).astype(np.float32)
+    ka, va = CB.aos_from_planar(cache)
+    kq, vq = O.planar_dequant(cache)
+    exp = O.paged_attention_ref(q, kq, vq, bt, np.array([L], np.int32), np.array([0, L], np.int32), 0.09)
+    G = Hq // Hkv
+    for h in range(Hkv):
+        K, V = CB.head_kv_cpu(ka, va, bt[0], L, h)
+        qh = torch.from_numpy(q[:, h * G:(h + 1) * G]).permute(1, 0, 2)
+        got = torch.cat([CB.prefill_chunk_cpu(qh, K, V, r0, min(r0 + 64, L), L, 0.09) for r0 in range(0, L, 64)], 1)
+        assert np.max(np.abs(got.permute(1, 0, 2).numpy() - exp[:, h * G:(h + 1) * G])) < 1e-4
+    secs, flop, heads, done, nch, g, thr = CB.time_cpu_prefill(torch.from_numpy(q), ka, va, bt[0], L, 0.09,
+                                                                chunk=64, budget_s=60.0)
+    assert (heads, done, nch, g) == (Hkv, Hkv * 3, 3, G) and secs > 0
+    assert flop == Hkv * 4.0 * 128 * G * (L * (L + 1) // 2)
+    assert thr == CB.host_threads() <= len(os.sched_getaffinity(0))
+
+
 def _flat_case(rng, B, Hq, Hkv, Sq, Skv):
     q = rng.standard_normal((B, Hq, Sq, 128)).astype(np.float32)
     k = rng.standard_normal((B, Hkv, Skv, 128)).astype(np.float16)
