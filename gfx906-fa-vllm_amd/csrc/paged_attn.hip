@@ -67,6 +67,7 @@ struct AttnParams {
     int causal;
     int Hkv, G, block_size;
     float scale_log2e;
+    float pf_qmul, pf_kmul;  // prefill: Q * 2^-e and K^ * (c * 2^e), c = scale_log2e (qmul * kmul = c)
     void *out;
     int64_t o_ts, o_hs;
     float *ws_ml, *ws_o;  // partial (m, l) and O per slot row
@@ -860,9 +861,13 @@ __device__ __forceinline__ void pf_fetch(PfRaw &r, const uint8_t *kb, const uint
     }
 }
 
-__device__ __forceinline__ half8_t scale8(half8_t v, half_t s) {
-    const half8_t sv = {s, s, s, s, s, s, s, s};
-    return v * sv;
+// v * s for exact fp16 v and an fp32 s: each product formed in fp32 and
+// rounded to fp16 once (v_fma_mix).
+__device__ __forceinline__ half8_t scale8_f32(half8_t v, float s) {
+    half8_t r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (half_t)fmaf((float)v[e], s, 0.0f);
+    return r;
 }
 
 // fp16 pair with Inf / NaN replaced by +-65504 (v_pk_max/min_f16 return the
@@ -877,16 +882,22 @@ __device__ __forceinline__ half2_t finite2(half2_t x) {
 // of the range, the only one that can hold keys past kv_end): bytes of tokens
 // past the valid range are dequantized as they are - their scores are masked
 // to -inf (P = 0) - and the V scales are made finite so that 0 * V^ stays 0.
-__device__ __forceinline__ void pf_dequant_k(const PfRaw &r, uint8_t *kst, int sp, int lane, int hf) {
+// K^ carries the part kmul = c * 2^e of the softmax scale c = scale * log2 e
+// (Q carries the exact power of two 2^-e): K^ = fp16(q * (d * kmul)), the
+// product formed in fp32 and rounded once.  Pre-scaling Q by c in fp16 would
+// add a second rounding to every score; this keeps fp16 / bf16 Q exact.
+__device__ __forceinline__ void pf_dequant_k(const PfRaw &r, uint8_t *kst, int sp, int lane, int hf,
+                                             float kmul) {
     const int t = lane & 15, g = lane >> 4;
     // (vector elements are copied to scalars before __builtin_bit_cast: a
     // bit_cast of an ext_vector element lvalue reads element 0 with this clang)
     const half2_t ks = __builtin_bit_cast(half2_t, r.ks);
+    const float s0 = (float)ks[0] * kmul, s1 = (float)ks[1] * kmul;
     const uint32_t k0 = r.k[0], k1 = r.k[1], k2 = r.k[2], k3 = r.k[3];
     // K^: row 16sp + t, d chunks 4b + g (8 fp16 each)
     uint8_t *krow = kst + (16 * sp + t) * PF_KPITCH + 16 * g + 128 * hf;
-    *reinterpret_cast<half8_t *>(krow) = scale8(i8x8_to_half8(k0, k1), ks[0]);
-    *reinterpret_cast<half8_t *>(krow + 64) = scale8(i8x8_to_half8(k2, k3), ks[1]);
+    *reinterpret_cast<half8_t *>(krow) = scale8_f32(i8x8_to_half8(k0, k1), s0);
+    *reinterpret_cast<half8_t *>(krow + 64) = scale8_f32(i8x8_to_half8(k2, k3), s1);
 }
 
 template <bool TAIL, bool VF16>
@@ -975,7 +986,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     const int lim = rvalid ? (p.causal ? min(sl - 1, qa + j) : sl - 1) : INT32_MAX;
     half8_t qf[8];
     {
-        const float c = p.scale_log2e;
+        const float c = p.pf_qmul;  // a power of two: exact for fp16 / bf16 Q
         const int64_t qoff = (int64_t)(q0 + j) * p.q_ts + (int64_t)hq * p.q_hs + 8 * hb;
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
@@ -1020,7 +1031,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     struct PfRawT {
         PfRaw h[PF_BOTH ? 2 : 1];
     };
-    auto fetch = [&](PfRawT &rw, int kt) {
+    auto fetch = [&](PfRawT &rw, int kt) __attribute__((always_inline)) {
         const int rel = kt - cbase;  // 0..127, uniform
         const int pa = __builtin_amdgcn_readlane(pw0, rel & 63);
         const int pb = __builtin_amdgcn_readlane(pw1, rel & 63);
@@ -1031,11 +1042,11 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
         pf_fetch<VF16>(rw.h[0], kb, vb, lane, hf);
         if constexpr (PF_BOTH) pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
     };
-    auto dequant_k = [&](const PfRawT &rw, uint8_t *kst) {
-        pf_dequant_k(rw.h[0], kst, wsp, lane, hf);
-        if constexpr (PF_BOTH) pf_dequant_k(rw.h[1], kst, wsp, lane, 1);
+    auto dequant_k = [&](const PfRawT &rw, uint8_t *kst) __attribute__((always_inline)) {
+        pf_dequant_k(rw.h[0], kst, wsp, lane, hf, p.pf_kmul);
+        if constexpr (PF_BOTH) pf_dequant_k(rw.h[1], kst, wsp, lane, 1, p.pf_kmul);
     };
-    auto dequant_v = [&](const PfRawT &rw, uint8_t *vst, auto tail) {
+    auto dequant_v = [&](const PfRawT &rw, uint8_t *vst, auto tail) __attribute__((always_inline)) {
         constexpr bool T = decltype(tail)::value;
         pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, hf);
         if constexpr (PF_BOTH) pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
@@ -1057,7 +1068,8 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     const int vread = (lane & 31) * PF_VPITCH + 16 * hb;  // + 32*dt*VPITCH + 16*(4st+2sg)
 
     // One pipeline step: loads of tile kt+2 into rf, dequant of tile kt+1
-    // from rd, attention over tile kt.
+    // from rd, attention over tile kt.  (The tile lambdas are forced inline:
+    // an outlined step passes its state through scratch.)
     // mode: 0 = fetch tile kt+2 and dequantize tile kt+1 (a full tile),
     //       1 = same, tile kt+1 being the last (tail) tile,
     //       2 = nothing left to fetch or dequantize
@@ -1066,7 +1078,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     // tiles through a second copy of the tile loop (guard), so full row tiles
     // keep the unbranched schedule.
     const bool wact = row0 + 32 * w < nrows;  // uniform over the wave
-    auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode, auto guard) {
+    auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode, auto guard) __attribute__((always_inline)) {
         // odd: kt & 1 (compile time) - read stages kt&1, write stages (kt+1)&1
         const uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
         const uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
@@ -1203,7 +1215,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
         }
     }
     __syncthreads();
-    auto tiles = [&](auto g) {
+    auto tiles = [&](auto g) __attribute__((always_inline)) {
         // Main loop: pairs of tiles whose dequantized successors are full tiles.
         // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2.
         int kt = 0;
@@ -1642,6 +1654,17 @@ struct Plan {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Splits the softmax scale c between Q and K^ for the prefill kernel:
+// Q * 2^-e (exact) and K^ * (c * 2^e), with e chosen so that c * 2^e is in
+// [1, 2): K^ keeps about the magnitude of the dequantized keys.
+void set_prefill_scale(AttnParams &p) {
+    int e = 0;
+    (void)frexpf(p.scale_log2e, &e);  // c = m * 2^e, m in [0.5, 1)
+    e = max(-60, min(60, 1 - e));
+    p.pf_qmul = ldexpf(1.0f, -e);
+    p.pf_kmul = ldexpf(p.scale_log2e, e);
+}
+
 // CUs of the current device, queried once per device.  Threads may race on
 // the first query of a device; they store the same value, and the relaxed
 // atomics make that race well defined.  256 (MI355X) when no device is
@@ -1913,6 +1936,7 @@ hipError_t paged_attention_impl(
     p.G = G;
     p.block_size = block_size;
     p.scale_log2e = scale * LOG2E;
+    set_prefill_scale(p);
     p.out = out;
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
@@ -2069,6 +2093,7 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_tiled(
     p.G = num_heads / num_kv_heads;
     p.block_size = block_size;
     p.scale_log2e = scale * LOG2E;
+    set_prefill_scale(p);
     p.out = out;
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
