@@ -31,6 +31,7 @@
 //                        K/V tiles dequantized to fp16 in LDS; 32x32x16 MFMA
 #include <atomic>
 #include <cstdio>
+#include <mutex>
 #include <type_traits>
 
 #include "q8_common.h"
@@ -1857,6 +1858,39 @@ extern "C" int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tok
 
 namespace {
 
+// Scratch of gfx906_fa_amd_paged_attention_noalloc: the workspace of every
+// call on a device, one copy per device (each device that runs this code
+// object holds it until the process ends).  No initial contents are needed:
+// each call writes what it reads.  In host code `scratch` names a host-side
+// stand-in; its device address comes from hipGetSymbolAddress, once per
+// device, with that device current.
+static __device__ __align__(256) uint8_t scratch[GFX906_FA_AMD_SCRATCH_BYTES];
+
+hipError_t scratch_address(void **out) {
+    static std::atomic<void *> addr[64];
+    static std::mutex mu;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    void *a = addr[dev].load(std::memory_order_acquire);
+    if (a == nullptr) {
+        std::lock_guard<std::mutex> lock(mu);
+        a = addr[dev].load(std::memory_order_relaxed);
+        if (a == nullptr) {
+            e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || a == nullptr) {
+                fprintf(stderr, "[gfx906_fa_amd] paged_attention_noalloc: hipGetSymbolAddress(scratch) failed (%d)\n",
+                        (int)e);
+                return e != hipSuccess ? e : hipErrorInvalidSymbol;
+            }
+            addr[dev].store(a, std::memory_order_release);
+        }
+    }
+    *out = a;
+    return hipSuccess;
+}
+
 // The step's new K/V rows for the fused cache write (element strides).
 struct NewKV {
     const void *key, *value;
@@ -1873,7 +1907,7 @@ hipError_t paged_attention_impl(
     int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
     int block_size, int max_query_len, int max_seq_len, float scale, void *out, int out_dtype,
     int64_t out_token_stride, int64_t out_head_stride, void *workspace, size_t workspace_bytes,
-    const NewKV *nkv, hipStream_t stream) {
+    const NewKV *nkv, hipStream_t stream, bool noalloc = false) {
     if (nkv && num_tokens > 0) {
         const uint64_t align = nkv->dtype == GFA_DTYPE_F32 ? 8 : 4;  // two values per lane
         if (nkv->dtype != q_dtype ||
@@ -1910,7 +1944,23 @@ hipError_t paged_attention_impl(
         return hipErrorInvalidValue;
     }
     const int G = num_heads / num_kv_heads;
-    const Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1));
+    Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1));
+    if (noalloc) {
+        // the library's scratch array instead of a caller workspace; a plan
+        // whose split-prefill partials do not fit leaves row tiles unsplit
+        if (pl.bytes > GFX906_FA_AMD_SCRATCH_BYTES)
+            pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1), false);
+        if (pl.bytes > GFX906_FA_AMD_SCRATCH_BYTES) {
+            fprintf(stderr,
+                    "[gfx906_fa_amd] paged_attention_noalloc: this batch needs %zu bytes of scratch, more than "
+                    "the library's %zu (use gfx906_fa_amd_paged_attention with a workspace)\n",
+                    pl.bytes, (size_t)GFX906_FA_AMD_SCRATCH_BYTES);
+            return hipErrorInvalidValue;
+        }
+        const hipError_t e = scratch_address(&workspace);
+        if (e != hipSuccess) return e;
+        workspace_bytes = GFX906_FA_AMD_SCRATCH_BYTES;
+    }
     if (workspace == nullptr || workspace_bytes < pl.bytes || ((uintptr_t)workspace & 255u)) {
         fprintf(stderr, "[gfx906_fa_amd] paged_attention: workspace of %zu bytes (256-aligned) required, got %zu\n",
                 pl.bytes, workspace_bytes);
@@ -2018,6 +2068,22 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention(
                                 num_heads, num_kv_heads, head_size, block_size, max_query_len, max_seq_len,
                                 scale, out, out_dtype, out_token_stride, out_head_stride, workspace,
                                 workspace_bytes, nullptr, stream);
+}
+
+extern "C" hipError_t gfx906_fa_amd_paged_attention_noalloc(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
+    int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *q_abs_offset,
+    int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
+    int block_size, int max_query_len, int max_seq_len, float scale, void *out, int out_dtype,
+    int64_t out_token_stride, int64_t out_head_stride, hipStream_t stream) {
+    return paged_attention_impl(q, q_dtype, q_token_stride, q_head_stride, k_cache, v_cache,
+                                cache_block_stride, cache_head_stride, block_table, block_table_stride,
+                                seq_lens, query_start_loc, q_abs_offset, causal, num_seqs, num_tokens,
+                                num_heads, num_kv_heads, head_size, block_size, max_query_len, max_seq_len,
+                                scale, out, out_dtype, out_token_stride, out_head_stride, nullptr, 0,
+                                nullptr, stream, true);
 }
 
 extern "C" hipError_t gfx906_fa_amd_paged_attention_kv_write(

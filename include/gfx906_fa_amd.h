@@ -244,6 +244,33 @@ hipError_t gfx906_fa_amd_paged_attention(
     void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
     void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* (5n) (5) with no workspace argument and no allocation of any kind.  No
+ *      counterpart in the reference: it is for callers that cannot allocate
+ *      (code under HIP graph capture, tight serving loops, harnesses that
+ *      forbid hipMalloc).  The workspace is the library's own scratch, a
+ *      file-scope device array of GFX906_FA_AMD_SCRATCH_BYTES (64 MiB), one
+ *      copy per device, held by every device the library runs on until the
+ *      process ends.  Decode / verify plans are those of (5), so outputs
+ *      are bit-identical to (5); a batch whose split-prefill partials would
+ *      not fit in the scratch runs its prefill row tiles unsplit (same
+ *      tolerance, different summation order).  A batch whose plan still
+ *      exceeds the scratch is rejected (hipErrorInvalidValue and a line on
+ *      stderr) before any work is enqueued.  Every call on a device shares
+ *      that device's scratch: calls that overlap on one device (concurrent
+ *      streams, several host threads) race and must be ordered by the
+ *      caller. */
+#define GFX906_FA_AMD_SCRATCH_BYTES ((size_t)64 << 20)
+
+hipError_t gfx906_fa_amd_paged_attention_noalloc(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride,
+    const uint8_t *k_cache, const uint8_t *v_cache, int64_t cache_block_stride,
+    int64_t cache_head_stride, const int32_t *block_table, int64_t block_table_stride,
+    const int32_t *seq_lens, const int32_t *query_start_loc, const int32_t *q_abs_offset,
+    int causal, int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
+    int head_size, int block_size, int max_query_len, int max_seq_len, float scale,
+    void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
+    hipStream_t stream);
+
 /* (5b) (4) followed by (5) in one call: key / value [num_tokens, Hkv, D] (the
  *      query dtype, element strides) are quantized to Q8_0 and written at
  *      slot_mapping[t] (< 0 = skip) before attention reads the cache.  When
