@@ -14,6 +14,7 @@ LIB = os.path.join(ROOT, "gfx906-fa-vllm_amd", "libgfx906_fa_amd.so")
 def _declared():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    src = re.sub(r"^\s*#.*$", "", src, flags=re.M)     # preprocessor lines (macros are not symbols)
     return sorted(set(re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", src)) -
                   {"extern", "if", "defined"})
 
@@ -25,7 +26,7 @@ def test_header_declares_expected_entry_points():
               "gfx906_fa_amd_paged_attention", "gfx906_fa_amd_paged_attention_workspace_size",
               "gfx906_fa_amd_gather_planar", "gfx906_fa_amd_gather_rows",
               "gfx906_fa_amd_paged_attention_workspace_bound", "gfx906_fa_amd_paged_attention_plan_info",
-              "gfx906_fa_amd_device_cus"]:
+              "gfx906_fa_amd_device_cus", "gfx906_fa_amd_paged_attention_noalloc"]:
         assert n in names
 
 
@@ -134,3 +135,10 @@ def test_ops_reject_cpu_tensors():
     import gfx906_fa
     with pytest.raises(RuntimeError, match="CUDA/HIP"):
         gfx906_fa.quantize_q8_0(torch.zeros(4, 32, dtype=torch.float16))
+
+
+def test_noalloc_scratch_size_stated():
+    """The allocation-free entry point's scratch is stated in the header."""
+    src = open(HEADER).read()
+    m = re.search(r"#define GFX906_FA_AMD_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", src)
+    assert m and int(m.group(1)) << int(m.group(2)) == 64 << 20
