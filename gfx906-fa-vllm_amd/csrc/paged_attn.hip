@@ -766,26 +766,29 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // ---------------------------------------------------------------------------
 // Prefill kernel: sequences with more than dec_rows_max packed rows.
 //
-// Workgroup = 8 waves x 32 rows = 256 consecutive packed rows of one
-// (sequence, kv-head).  K/V stream through LDS in 64-key tiles (four 16-token
+// Workgroup = 12 waves over 256 consecutive packed rows of one (sequence,
+// kv-head).  K/V stream through LDS in 64-key tiles (four 16-token
 // sub-pages), dequantized ONCE per workgroup to fp16 (K^ = q * d_k,
-// V^ = q * d_v, each rounded to fp16): wave w fetches and dequantizes half
-// w/4 (two Q8_0 blocks) of the K and V of sub-page w%4.  Every wave runs, per
-// tile,
-//   S'^T[64 keys x 32 rows] = K^ . Q^T - m   16 x v_mfma_f32_32x32x16_f16
-//   O^T[128 d x 32 rows]   += V^T . P^T      16 x v_mfma_f32_32x32x16_f16
-// with Q (pre-scaled by scale*log2 e) held in registers for the whole
-// kernel and the running row max m fed in as the accumulator input.
+// V^ = q * d_v, each rounded to fp16).  The waves have two roles:
+//   consumers (waves 0-7, two per SIMD): 32 query rows each; per tile
+//     S'^T[64 keys x 32 rows] = K^ . Q^T - m   16 x v_mfma_f32_32x32x16_f16
+//     O^T[128 d x 32 rows]   += V^T . P^T      16 x v_mfma_f32_32x32x16_f16
+//     with Q (pre-scaled by scale*log2 e) held in registers for the whole
+//     kernel and the running row max m fed in as the accumulator input;
+//   producers (waves 8-11, one per SIMD): wave 8 + i fetches sub-page i of
+//     every tile from HBM, PF_PDEPTH tiles ahead, and dequantizes it into
+//     the LDS stage the consumers read next.
+// A consumer's only LDS traffic is its MFMA operand reads, so the waits in
+// front of its MFMAs never queue behind dequant stores (LDS instructions of
+// one wave complete in order), and the dequant VALU work issues from a wave
+// of its own beside the two consumers' MFMAs.  The roles share one barrier
+// per tile: iteration kt, the consumers attend over tile kt (stage kt&1)
+// while the producers fill stage (kt+1)&1 with tile kt+1.
 // 32x32x16 operand layout (lane l, h = l/32): A[i = l%32][k = 8h+e],
 // B[k = 8h+e][j = l%32], D[i = 8(r/4)+4h+r%4][j = l%32] for register r.  A
 // lane's S^T registers 8s..8s+7 are then exactly the keys its P^T operand
 // needs for PV step s when the contraction order inside each 16 keys swaps
 // key bits 2 and 3; V^T is stored in LDS in that order.
-//
-// Software pipeline, one barrier per tile: iteration kt issues the HBM loads
-// of tile kt+2, dequantizes tile kt+1 (loaded one iteration earlier) into
-// the other LDS stage while the QK MFMAs of tile kt run, then the softmax
-// of tile kt overlaps its PV MFMAs.
 //
 // LDS tile (per stage):
 //   K^   [64 keys][272 B]  (128 fp16 + 16 B pad)
@@ -799,24 +802,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
-#ifndef GFA_PF_WAVES
-#define GFA_PF_WAVES 8
-#endif
-constexpr int PF_WAVES = GFA_PF_WAVES;        // 8 (2 waves per SIMD) or 4 (1 wave per SIMD)
-constexpr int PF_ROWS = 32 * PF_WAVES;
-#ifndef GFA_PF_SKIP
-#define GFA_PF_SKIP 1
-#endif
-#ifndef GFA_PF_TK
-#define GFA_PF_TK 64
-#endif
-constexpr int PF_TK = GFA_PF_TK;              // keys per LDS tile: 64 or 128
+constexpr int PF_CWAVES = 8;                  // consumer waves (32 rows each)
+constexpr int PF_PWAVES = 4;                  // producer waves (one sub-page of each tile)
+constexpr int PF_WAVES = PF_CWAVES + PF_PWAVES;
+constexpr int PF_ROWS = 32 * PF_CWAVES;
+constexpr int PF_TK = 64;                     // keys per LDS tile
 constexpr int PF_NSP = PF_TK / 16;            // sub-pages per tile
-// a wave fetches and dequantizes both halves of one sub-page per tile
-// (PF_NSP == PF_WAVES) or one half (2 * PF_NSP == PF_WAVES)
-constexpr bool PF_BOTH = PF_NSP == PF_WAVES;
-static_assert(PF_BOTH || 2 * PF_NSP == PF_WAVES, "tile / wave split");
+static_assert(PF_NSP == PF_PWAVES, "one producer wave per sub-page");
 constexpr int PF_NST = PF_TK / 32;            // 32-key S subtiles per tile
+#ifndef GFA_PF_PDEPTH
+#define GFA_PF_PDEPTH 4
+#endif
+constexpr int PF_PDEPTH = GFA_PF_PDEPTH;      // producer register ring: tiles fetched ahead + 1
+static_assert(PF_PDEPTH == 2 || PF_PDEPTH == 4, "ring depth: even, unrolled");
 constexpr int PF_KPITCH = 272;
 constexpr int PF_VPITCH = 2 * PF_TK + 16;
 constexpr int PF_KBYTES = PF_TK * PF_KPITCH;
@@ -937,10 +935,10 @@ __device__ __forceinline__ void pf_dequant_v(const PfRaw &r, uint8_t *vst, int s
 
 template <int QDT, int ODT, bool VF16, bool MASK>
 __global__ __launch_bounds__(64 * PF_WAVES)
-__attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefill_kernel(AttnParams p) {
+__attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p) {
     // two LDS stages of K^ and of V^, each a distinct object: the compiler
-    // can then prove that the dequant stores (one stage) and the MFMA operand
-    // reads (the other) are independent and interleave them
+    // can then prove that the stores into one and the reads of the other are
+    // independent
     __shared__ __attribute__((aligned(16))) uint8_t ldsk0[PF_KBYTES];
     __shared__ __attribute__((aligned(16))) uint8_t ldsk1[PF_KBYTES];
     __shared__ __attribute__((aligned(16))) uint8_t ldsv0[PF_VBYTES];
@@ -968,23 +966,170 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     if (row0 >= nrows) return;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int hb = lane >> 5;
     const int sl = p.seq_lens[s];
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
     const int jlast = (min(row0 + PF_ROWS, nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
     // key tiles [ktb, ktb + ntk) of the row tile's (kv_end + PF_TK - 1) / PF_TK;
-    // the loop below counts tiles from 0 and adds ktb where it needs a key index
+    // the loops below count tiles from 0 and add ktb where they need a key index
     const int ntk_all = (kv_end + PF_TK - 1) / PF_TK;
     const int ktb = min(kt0, ntk_all);
     const int ntk = min(kt1, ntk_all) - ktb;
+    using Even = std::integral_constant<bool, false>;
+    using Odd = std::integral_constant<bool, true>;
 
+    if (w >= PF_CWAVES) {
+        // ---- producer: sub-page wsp of every tile, both halves ----------
+        // Page ids come from two lane-distributed windows of 64 tiles (lane i
+        // of pw0 / pw1: the page of this wave's sub-page in tile cbase + i /
+        // cbase + 64 + i).  Tile t sits in ring slot t % PF_PDEPTH from its
+        // fetch until its dequant, one iteration before the consumers read it.
+        const int wsp = w - PF_CWAVES;
+#ifdef GFA_PF_PRIO
+        __builtin_amdgcn_s_setprio(GFA_PF_PRIO);
+#endif
+        const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
+        const int bs = p.block_size;
+        const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
+        const int spb = PF_NSP * ktb + wsp;
+        auto sp_of = [&](int kt) { return min(PF_NSP * kt + spb, last_sp); };
+        auto load_pg = [&](int c) -> int {
+            const int kt = 64 * c + lane;
+            return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
+        };
+        // Waits for a window load right where it is issued (once per 64
+        // tiles): a window register still pending in the loop would make
+        // every v_readlane of it wait for all loads in flight (vmcnt counts in
+        // order), the K/V fetches included.
+        auto ready = [](int &v) { asm volatile("" : "+v"(v)); };
+        const uint8_t *kplane = p.kc + (int64_t)h * p.chs;
+        const uint8_t *vplane = p.vc + (int64_t)h * p.vchs;
+        constexpr int VSUB = VF16 ? 4096 : SUBPAGE_BYTES;  // V bytes per 16-token sub-page
+        int pw0 = 0, pw1 = 0, cbase = 0;
+        struct PfRawT {
+            PfRaw h[2];
+        };
+        PfRawT ring[PF_PDEPTH];
+        // Fetch of tile t (uniform, t < cbase + 128).  Tiles past the range
+        // read page 0 at the last valid sub-page's offset (their bytes are
+        // never dequantized into a stage that is read).  The steady-state
+        // loop fetches unconditionally: with the same number of loads on
+        // every path the compiler's vmcnt waits cover only the tile being
+        // dequantized, not the PF_PDEPTH - 1 tiles still in flight.
+        auto fetch = [&](PfRawT &rw, int t) __attribute__((always_inline)) {
+            const int rel = t - cbase;  // 0..127, uniform
+            const int pa = __builtin_amdgcn_readlane(pw0, rel & 63);
+            const int pb = __builtin_amdgcn_readlane(pw1, rel & 63);
+            const int64_t page = rel < 64 ? pa : pb;
+            const int64_t spi = ((16 * sp_of(t)) % bs) >> 4;
+            const uint8_t *kb = kplane + page * p.cbs + spi * SUBPAGE_BYTES;
+            const uint8_t *vb = vplane + page * p.vcbs + spi * VSUB;
+            pf_fetch<VF16>(rw.h[0], kb, vb, lane, 0);
+            pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
+        };
+        // keeps the fetches of tiles up to kt + 2 * PF_PDEPTH inside the
+        // windows: called at kt = 0 mod PF_PDEPTH (uniform), before the
+        // group of PF_PDEPTH half-step pairs that fetch those tiles
+        auto slide = [&](int kt) __attribute__((always_inline)) {
+            if (kt - cbase >= 64) {
+                cbase += 64;
+                pw0 = pw1;
+                pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
+                ready(pw1);
+            }
+        };
+        // dequantizes the K (or V) half of tile t (in the ring) into stage t & 1
+        auto dequant_k = [&](const PfRawT &rw, auto odd) __attribute__((always_inline)) {
+            uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
+            pf_dequant_k(rw.h[0], kst, wsp, lane, 0, p.pf_kmul);
+            pf_dequant_k(rw.h[1], kst, wsp, lane, 1, p.pf_kmul);
+        };
+        auto dequant_v = [&](const PfRawT &rw, auto odd, auto tail) __attribute__((always_inline)) {
+            uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
+            constexpr bool T = decltype(tail)::value;
+            pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, 0);
+            pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
+        };
+        using NoTail = std::integral_constant<bool, false>;
+        using IsTail = std::integral_constant<bool, true>;
+        if (ntk > 0) {
+            pw0 = load_pg(0);
+            pw1 = ntk > 64 ? load_pg(1) : 0;
+            ready(pw0);
+            ready(pw1);
+#pragma unroll
+            for (int i = 0; i < PF_PDEPTH; ++i) fetch(ring[i], i);
+            dequant_k(ring[0], Even{});
+            if (ntk == 1) dequant_v(ring[0], Even{}, IsTail{});
+            else dequant_v(ring[0], Even{}, NoTail{});
+            fetch(ring[0], PF_PDEPTH);
+        }
+        __syncthreads();
+        // Half-steps h = 0 .. 2 ntk (a barrier each): K^ of tile t is written in
+        // h = 2t - 2 and V^ in h = 2t - 1, one half-step before consumer group
+        // A reads them (the stage each overwrites was last read in the
+        // half-step before).  After V^ of tile t its ring slot takes tile
+        // t + PF_PDEPTH.
+        auto hstep = [&](int t, auto slot_c) __attribute__((always_inline)) {
+            constexpr int SL = decltype(slot_c)::value;  // t % PF_PDEPTH
+            using StageOdd = std::integral_constant<bool, (SL & 1) != 0>;
+            dequant_k(ring[SL], StageOdd{});
+            __syncthreads();
+            dequant_v(ring[SL], StageOdd{}, NoTail{});
+            fetch(ring[SL], t + PF_PDEPTH);
+            __syncthreads();
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1 % PF_PDEPTH>;
+        using S2 = std::integral_constant<int, 2 % PF_PDEPTH>;
+        using S3 = std::integral_constant<int, 3 % PF_PDEPTH>;
+        // tiles 1 .. ntk - 2 (full), then the tail tile ntk - 1
+        int t = 1;
+        for (; t + PF_PDEPTH <= ntk - 1; t += PF_PDEPTH) {
+            slide(t - 1);
+            hstep(t, S1{});
+            hstep(t + 1, S2{});
+            if constexpr (PF_PDEPTH == 4) {
+                hstep(t + 2, S3{});
+                hstep(t + 3, S0{});
+            }
+        }
+        slide(t - 1);
+        const int rem = ntk - 1 - t;  // 0 .. PF_PDEPTH - 1 (uniform)
+        if (rem >= 1) hstep(t, S1{});
+        if constexpr (PF_PDEPTH == 4) {
+            if (rem >= 2) hstep(t + 1, S2{});
+            if (rem >= 3) hstep(t + 2, S3{});
+        }
+        if (ntk >= 2) {  // tile ntk - 1 from slot (ntk - 1) % PF_PDEPTH
+            switch ((ntk - 1) % PF_PDEPTH) {
+            case 0: dequant_k(ring[0], Even{}); __syncthreads(); dequant_v(ring[0], Even{}, IsTail{}); break;
+            case 1: dequant_k(ring[1 % PF_PDEPTH], Odd{}); __syncthreads(); dequant_v(ring[1 % PF_PDEPTH], Odd{}, IsTail{}); break;
+            case 2: dequant_k(ring[2 % PF_PDEPTH], Even{}); __syncthreads(); dequant_v(ring[2 % PF_PDEPTH], Even{}, IsTail{}); break;
+            default: dequant_k(ring[3 % PF_PDEPTH], Odd{}); __syncthreads(); dequant_v(ring[3 % PF_PDEPTH], Odd{}, IsTail{}); break;
+            }
+            __syncthreads();
+        }
+        // the half-steps 2 ntk - 2 .. 2 ntk hold no producer work
+        for (int i = ntk >= 1 ? 3 : 1; i > 0; --i) __syncthreads();
+        return;
+    }
+
+    // ---- consumer: 32 query rows ----------------------------------------
+    const int hb = lane >> 5;
     // this lane's query row, its causal bound and its Q^T fragments
     const int r = row0 + 32 * w + (lane & 31);
     const bool rvalid = r < nrows;
     const int j = rvalid ? r / p.G : 0;
     const int hq = h * p.G + (rvalid ? r - j * p.G : 0);
     const int lim = rvalid ? (p.causal ? min(sl - 1, qa + j) : sl - 1) : INT32_MAX;
+    const bool wact = row0 + 32 * w < nrows;  // uniform over the wave
+    if (!wact) {
+        // all 32 rows past the sequence's rows (its last row tile): keep the
+        // workgroup's barrier count
+        for (int i = 0; i < 2 * ntk + 2; ++i) __syncthreads();
+        return;
+    }
     half8_t qf[8];
     {
         const float c = p.pf_qmul;  // a power of two: exact for fp16 / bf16 Q
@@ -992,8 +1137,10 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                qf[kk][e] = rvalid ? (half_t)(load_as_f32<QDT>(p.q, qoff + 16 * kk + e) * c) : (half_t)0.0f;
+            for (int e = 0; e < 8; ++e) {  // (row j = 0 stands in for rows past nrows: a valid address)
+                const float v = load_as_f32<QDT>(p.q, qoff + 16 * kk + e);
+                qf[kk][e] = rvalid ? (half_t)(v * c) : (half_t)0.0f;
+            }
         }
     }
     int lim_min;  // smallest bound over the wave's rows: tiles below it need no mask
@@ -1001,57 +1148,6 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
         const float f = (float)min(lim, 1 << 24);
         lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
     }
-
-    // Wave w fetches and dequantizes half hf = w/4 of sub-page w%4 of every
-    // tile (K and V).  Page ids come from two lane-distributed windows of 64
-    // tiles (lane i of pw0 / pw1: the page of this wave's sub-page in tile
-    // cbase + i / cbase + 64 + i); tiles past the range read page 0 (their
-    // bytes land in an LDS stage that is never read).
-    const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
-    const int bs = p.block_size;
-    const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
-    // 8 waves over 64-key tiles: wave w takes half w/4 of sub-page w%4;
-    // otherwise wave w takes both halves of sub-page w
-    const int wsp = PF_BOTH ? w : w % PF_NSP;
-    const int hf = PF_BOTH ? 0 : w / PF_NSP;
-    const int spb = PF_NSP * ktb + wsp;
-    auto sp_of = [&](int kt) { return min(PF_NSP * kt + spb, last_sp); };
-    auto load_pg = [&](int c) -> int {
-        const int kt = 64 * c + lane;
-        return kt < ntk ? btrow[(16 * sp_of(kt)) / bs] : 0;
-    };
-    const uint8_t *kplane = p.kc + (int64_t)h * p.chs;
-    const uint8_t *vplane = p.vc + (int64_t)h * p.vchs;
-    constexpr int VSUB = VF16 ? 4096 : SUBPAGE_BYTES;  // V bytes per 16-token sub-page
-    int pw0 = 0, pw1 = 0, cbase = 0;
-    // Waits for a window load right where it is issued (once per 64 tiles):
-    // a window register still pending inside the loop would make every
-    // v_readlane of it wait for all loads in flight (vmcnt counts in order),
-    // the K/V fetches of the previous step included.
-    auto ready = [](int &v) { asm volatile("" : "+v"(v)); };
-    struct PfRawT {
-        PfRaw h[PF_BOTH ? 2 : 1];
-    };
-    auto fetch = [&](PfRawT &rw, int kt) __attribute__((always_inline)) {
-        const int rel = kt - cbase;  // 0..127, uniform
-        const int pa = __builtin_amdgcn_readlane(pw0, rel & 63);
-        const int pb = __builtin_amdgcn_readlane(pw1, rel & 63);
-        const int64_t page = rel < 64 ? pa : pb;
-        const int64_t spi = ((16 * sp_of(kt)) % bs) >> 4;
-        const uint8_t *kb = kplane + page * p.cbs + spi * SUBPAGE_BYTES;
-        const uint8_t *vb = vplane + page * p.vcbs + spi * VSUB;
-        pf_fetch<VF16>(rw.h[0], kb, vb, lane, hf);
-        if constexpr (PF_BOTH) pf_fetch<VF16>(rw.h[1], kb, vb, lane, 1);
-    };
-    auto dequant_k = [&](const PfRawT &rw, uint8_t *kst) __attribute__((always_inline)) {
-        pf_dequant_k(rw.h[0], kst, wsp, lane, hf, p.pf_kmul);
-        if constexpr (PF_BOTH) pf_dequant_k(rw.h[1], kst, wsp, lane, 1, p.pf_kmul);
-    };
-    auto dequant_v = [&](const PfRawT &rw, uint8_t *vst, auto tail) __attribute__((always_inline)) {
-        constexpr bool T = decltype(tail)::value;
-        pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, hf);
-        if constexpr (PF_BOTH) pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
-    };
 
     float16v_t o[4];
 #pragma unroll
@@ -1065,42 +1161,23 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
     bool has_m = false;
 
     // lane-constant LDS offsets of the MFMA operands
-    const int kread = (lane & 31) * PF_KPITCH + 16 * hb;            // + 32*st*KPITCH + 32*kk
+    const int kread = (lane & 31) * PF_KPITCH + 16 * hb;  // + 32*st*KPITCH + 32*kk
     const int vread = (lane & 31) * PF_VPITCH + 16 * hb;  // + 32*dt*VPITCH + 16*(4st+2sg)
 
-    // One pipeline step: loads of tile kt+2 into rf, dequant of tile kt+1
-    // from rd, attention over tile kt.  (The tile lambdas are forced inline:
-    // an outlined step passes its state through scratch.)
-    // mode: 0 = fetch tile kt+2 and dequantize tile kt+1 (a full tile),
-    //       1 = same, tile kt+1 being the last (tail) tile,
-    //       2 = nothing left to fetch or dequantize
-    // A wave whose 32 rows are all past the sequence's rows (the last row tile
-    // of a sequence) only fetches and dequantizes: the workgroup runs such
-    // tiles through a second copy of the tile loop (guard), so full row tiles
-    // keep the unbranched schedule.
-    const bool wact = row0 + 32 * w < nrows;  // uniform over the wave
-    auto step = [&](int kt, PfRawT &rf, const PfRawT &rd, auto odd, auto mode, auto guard) __attribute__((always_inline)) {
-        // odd: kt & 1 (compile time) - read stages kt&1, write stages (kt+1)&1
+    // The two consumer waves of a SIMD run half a tile apart: group A (waves
+    // 0-3) computes S' of tile kt in half-step 2kt and its softmax + PV in
+    // half-step 2kt + 1; group B (waves 4-7) one half-step later.  Each
+    // half-step a SIMD then holds one wave's QK MFMAs and the other's
+    // exponentials and PV MFMAs.
+    float16v_t sacc[PF_NST];  // S' of the tile between its two half-steps
+    // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile (stage kt & 1)
+    auto qk = [&](auto odd) __attribute__((always_inline)) {
         const uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
-        const uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
-        uint8_t *wkst = decltype(odd)::value ? ldsk0 : ldsk1;
-        uint8_t *wvst = decltype(odd)::value ? ldsv0 : ldsv1;
-        constexpr int MODE = decltype(mode)::value;
-        using TailV = std::integral_constant<bool, MODE == 1>;
-        if constexpr (MODE != 2) {
-            fetch(rf, kt + 2);
-            dequant_k(rd, wkst);
-            dequant_v(rd, wvst, TailV{});
-        }
-
-        // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile
-        float16v_t sacc[PF_NST];
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
-            {   // -m in all 16 accumulator registers, built as a 64-bit splat:
-                // the compiler then builds it once per tile, feeds it to the
-                // first MFMA of both chains as srcC and keeps the kernel
-                // spill-free (a float splat was rebuilt per chain, 32 moves)
+            {   // -m in all 16 accumulator registers, built as a 64-bit splat
+                // (the compiler then builds it once per tile and feeds it to
+                // the first MFMA of both chains as srcC)
                 const uint64_t pr = ((uint64_t)__float_as_uint(-m_use) << 32) | __float_as_uint(-m_use);
                 u64x8_t sp;
 #pragma unroll
@@ -1113,14 +1190,10 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
-        // past here an idle wave skips (the branch after the QK MFMAs keeps
-        // the dequant of the next tile interleaved with them)
-        if constexpr (decltype(guard)::value) {
-            if (!wact) {
-                __syncthreads();
-                return;
-            }
-        }
+    };
+    // softmax and O += P V^ over tile kt (stage kt & 1)
+    auto sv = [&](int kt, auto odd) __attribute__((always_inline)) {
+        const uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
         const int kbase_t = PF_TK * (kt + ktb);
         if constexpr (MASK) {  // S' += mask[s][j][key] (natural log units -> log2)
             const uint16_t *mrow = p.mask + (int64_t)s * p.mask_bs + (int64_t)j * p.mask_rs;
@@ -1166,9 +1239,7 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
             for (int st = 0; st < PF_NST; ++st) sacc[st] -= delta;
         }
         // Row sum of the fp16-rounded p with v_dot2 (the same values the PV
-        // MFMAs consume).  v_dot2 issues to the matrix pipe; plain fp32 adds
-        // of the unrounded p instead (which do issue under MFMAs) measured
-        // 0.7 % slower on the same box.
+        // MFMAs consume).
         const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
         float tsum = 0.0f;
 #pragma unroll
@@ -1193,64 +1264,30 @@ __attribute__((amdgpu_waves_per_eu(PF_WAVES / 4, PF_WAVES / 4))) void attn_prefi
             }
         }
         l_run += tsum;
-        __syncthreads();
     };
-    using Even = std::integral_constant<bool, false>;
-    using Odd = std::integral_constant<bool, true>;
-    using Full = std::integral_constant<int, 0>;
-    using Tail = std::integral_constant<int, 1>;
-    using Last = std::integral_constant<int, 2>;
-    PfRawT r0, r1;
-    if (ntk > 0) {
-        pw0 = load_pg(0);
-        pw1 = ntk > 64 ? load_pg(1) : 0;
-        ready(pw0);
-        ready(pw1);
-        fetch(r0, 0);
-        dequant_k(r0, ldsk0);
-        if (ntk > 1) {
-            fetch(r1, 1);
-            dequant_v(r0, ldsv0, std::integral_constant<bool, false>{});
-        } else {
-            dequant_v(r0, ldsv0, std::integral_constant<bool, true>{});
+    __syncthreads();  // the producers' first tile
+    const bool grp_b = w >= PF_CWAVES / 2;  // uniform over the wave
+    if (grp_b) __syncthreads();  // half-step 0
+    {
+        int kt = 0;
+        for (; kt + 2 <= ntk; kt += 2) {
+            qk(Even{});
+            __syncthreads();
+            sv(kt, Even{});
+            __syncthreads();
+            qk(Odd{});
+            __syncthreads();
+            sv(kt + 1, Odd{});
+            __syncthreads();
+        }
+        if (kt < ntk) {
+            qk(Even{});
+            __syncthreads();
+            sv(kt, Even{});
+            __syncthreads();
         }
     }
-    __syncthreads();
-    auto tiles = [&](auto g) __attribute__((always_inline)) {
-        // Main loop: pairs of tiles whose dequantized successors are full tiles.
-        // r1 holds tile kt+1; r0 (tile kt, dequantized) takes tile kt+2.
-        int kt = 0;
-        for (; kt + 3 < ntk; kt += 2) {
-            step(kt, r0, r1, Even{}, Full{}, g);
-            step(kt + 1, r1, r0, Odd{}, Full{}, g);
-            if (kt + 2 - cbase >= 64) {  // slide the page windows (uniform)
-                cbase += 64;
-                pw0 = pw1;
-                pw1 = cbase + 64 < ntk ? load_pg(cbase / 64 + 1) : 0;
-                ready(pw1);
-            }
-        }
-        // the last 1-3 tiles (uniform)
-        const int rem = ntk - kt;
-        if (rem == 3) {
-            step(kt, r0, r1, Even{}, Full{}, g);
-            step(kt + 1, r1, r0, Odd{}, Tail{}, g);
-            step(kt + 2, r0, r1, Even{}, Last{}, g);
-        } else if (rem == 2) {
-            step(kt, r0, r1, Even{}, Tail{}, g);
-            step(kt + 1, r1, r0, Odd{}, Last{}, g);
-        } else if (rem == 1) {
-            step(kt, r0, r1, Even{}, Last{}, g);
-        }
-    };
-#if GFA_PF_SKIP == 2
-    if (row0 + PF_ROWS <= nrows) tiles(std::false_type{});
-    else tiles(std::true_type{});
-#elif GFA_PF_SKIP == 1
-    tiles(std::true_type{});
-#else
-    tiles(std::false_type{});
-#endif
+    if (!grp_b) __syncthreads();  // half-step 2 ntk (group B's last softmax)
 
     // normalise and store: register e of d-tile dt is d = 32dt + 8(e/4) + 4hb + e%4
     {
