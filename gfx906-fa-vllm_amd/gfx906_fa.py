@@ -622,4 +622,167 @@ def forward_paged_direct(q: torch.Tensor, key_cache_q8: torch.Tensor, value_cach
     return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
 
 
+# ---------------------------------------------------------------------------
+# PyTorch custom ops: torch.ops.gfx906_fa.*
+# ---------------------------------------------------------------------------
+# The ops above as torch.library custom ops, so torch.compile / torch.export
+# trace them as opaque nodes (the reference registers its ops through a torch
+# extension module, extension/gfx906_fa.cpp:660-690).  Each op runs the
+# function of the same name above; a fake implementation gives the output
+# shapes for tracing.  Custom ops may not return an alias of an input, so the
+# ops that can write into caller buffers come in a functional form (outputs
+# allocated) and an ``_out`` form (outputs written in place, nothing returned).
+# In-place arguments are declared in each schema: caches, workspaces, outputs
+# and the query / key the fused rotary write rotates.  An in-place argument
+# that may be None (the workspace) has no default: torch's in-place
+# bookkeeping indexes it positionally, so callers pass it, None included.
+_NS = "gfx906_fa"
+
+
+def _register_torch_ops() -> None:
+    from torch.library import custom_op
+
+    @custom_op(f"{_NS}::quantize_q8_0", mutates_args=())
+    def _quantize_q8_0(k_fp16: torch.Tensor) -> torch.Tensor:
+        return quantize_q8_0(k_fp16)
+
+    @_quantize_q8_0.register_fake
+    def _(k_fp16):
+        D = k_fp16.shape[-1]
+        return k_fp16.new_empty((*k_fp16.shape[:-1], D // QK8_0 * Q8_0_BYTES), dtype=torch.uint8)
+
+    @custom_op(f"{_NS}::reshape_and_cache_q8", mutates_args=("k_cache_q8",))
+    def _reshape_and_cache_q8(key: torch.Tensor, slot_mapping: torch.Tensor, k_cache_q8: torch.Tensor) -> None:
+        reshape_and_cache_q8(key, slot_mapping, k_cache_q8)
+
+    @_reshape_and_cache_q8.register_fake
+    def _(key, slot_mapping, k_cache_q8):
+        return None
+
+    def _gather_shapes(key_cache_q8, value_cache, block_table, Sk):
+        B = block_table.shape[0]
+        _, _, Hkv, bpr = key_cache_q8.shape
+        return (B, Hkv, Sk, bpr), (B, Hkv, Sk, value_cache.shape[3])
+
+    @custom_op(f"{_NS}::gather_paged_kv_q8", mutates_args=())
+    def _gather_paged_kv_q8(key_cache_q8: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
+                            seq_lens: torch.Tensor, Sk: int) -> tuple[torch.Tensor, torch.Tensor]:
+        k, v = gather_paged_kv_q8(key_cache_q8, value_cache, block_table, seq_lens, Sk)
+        return k, v
+
+    @_gather_paged_kv_q8.register_fake
+    def _(key_cache_q8, value_cache, block_table, seq_lens, Sk):
+        ks, vs = _gather_shapes(key_cache_q8, value_cache, block_table, Sk)
+        return key_cache_q8.new_empty(ks), value_cache.new_empty(vs)
+
+    @custom_op(f"{_NS}::gather_paged_kv_q8_out", mutates_args=("k_out", "v_out"))
+    def _gather_paged_kv_q8_out(key_cache_q8: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
+                                seq_lens: torch.Tensor, Sk: int, k_out: torch.Tensor, v_out: torch.Tensor) -> None:
+        k, v = gather_paged_kv_q8(key_cache_q8, value_cache, block_table, seq_lens, Sk, k_out, v_out)
+        _check(k.data_ptr() == k_out.data_ptr() and v.data_ptr() == v_out.data_ptr(),
+               "gather_paged_kv_q8_out: k_out / v_out must be contiguous [B, Hkv, Sk, row] of the cache dtypes")
+
+    @_gather_paged_kv_q8_out.register_fake
+    def _(key_cache_q8, value_cache, block_table, seq_lens, Sk, k_out, v_out):
+        return None
+
+    @custom_op(f"{_NS}::forward", mutates_args=())
+    def _forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: float, kv_max: Optional[torch.Tensor] = None,
+                 mask: Optional[torch.Tensor] = None, q_abs_offset: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return forward(q, k_q8, v_fp16, scale, kv_max, mask, q_abs_offset)
+
+    @_forward.register_fake
+    def _(q, k_q8, v_fp16, scale, kv_max=None, mask=None, q_abs_offset=None):
+        return q.new_empty(q.shape, dtype=torch.float32)
+
+    @custom_op(f"{_NS}::forward_paged_direct", mutates_args=())
+    def _forward_paged_direct(q: torch.Tensor, key_cache_q8: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
+                              seq_lens: torch.Tensor, scale: float, mask: Optional[torch.Tensor] = None,
+                              q_abs_offset: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return forward_paged_direct(q, key_cache_q8, value_cache, block_table, seq_lens, scale, mask,
+                                    q_abs_offset)
+
+    @_forward_paged_direct.register_fake
+    def _(q, key_cache_q8, value_cache, block_table, seq_lens, scale, mask=None, q_abs_offset=None):
+        return q.new_empty(q.shape, dtype=torch.float32)
+
+    @custom_op(f"{_NS}::reshape_and_cache_q8_kv", mutates_args=("key_cache", "value_cache"))
+    def _reshape_and_cache_q8_kv(key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor, key_cache: torch.Tensor,
+                                 value_cache: torch.Tensor) -> None:
+        reshape_and_cache_q8_kv(key, value, slot_mapping, key_cache, value_cache)
+
+    @_reshape_and_cache_q8_kv.register_fake
+    def _(key, value, slot_mapping, key_cache, value_cache):
+        return None
+
+    @custom_op(f"{_NS}::rope_and_cache_q8_kv", mutates_args=("query", "key", "key_cache", "value_cache"))
+    def _rope_and_cache_q8_kv(positions: torch.Tensor, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                              cos_sin_cache: torch.Tensor, is_neox: bool, slot_mapping: torch.Tensor, key_cache: torch.Tensor,
+                              value_cache: torch.Tensor, rot_dim: Optional[int] = None) -> None:
+        rope_and_cache_q8_kv(positions, query, key, value, cos_sin_cache, is_neox, slot_mapping, key_cache,
+                             value_cache, rot_dim)
+
+    @_rope_and_cache_q8_kv.register_fake
+    def _(positions, query, key, value, cos_sin_cache, is_neox, slot_mapping, key_cache, value_cache,
+          rot_dim=None):
+        return None
+
+    @custom_op(f"{_NS}::gather_paged_kv_q8q8", mutates_args=())
+    def _gather_paged_kv_q8q8(key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                              Sk: int) -> tuple[torch.Tensor, torch.Tensor]:
+        k, v = gather_paged_kv_q8q8(key_cache, value_cache, block_table, seq_lens, Sk)
+        return k, v
+
+    @_gather_paged_kv_q8q8.register_fake
+    def _(key_cache, value_cache, block_table, seq_lens, Sk):
+        shape = (block_table.shape[0], key_cache.shape[1], Sk, 136)
+        return key_cache.new_empty(shape), key_cache.new_empty(shape)
+
+    @custom_op(f"{_NS}::paged_attention", mutates_args=("workspace",))
+    def _paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
+                         seq_lens: torch.Tensor, query_start_loc: torch.Tensor, max_query_len: int, max_seq_len: int,
+                         scale: float, workspace: Optional[torch.Tensor],
+                         q_abs_offset: Optional[torch.Tensor] = None, causal: bool = True,
+                         out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        return paged_attention(query, key_cache, value_cache, block_table, seq_lens, query_start_loc,
+                               max_query_len, max_seq_len, scale, workspace=workspace,
+                               q_abs_offset=q_abs_offset, causal=causal, out_dtype=out_dtype)
+
+    @_paged_attention.register_fake
+    def _(query, key_cache, value_cache, block_table, seq_lens, query_start_loc, max_query_len, max_seq_len,
+          scale, workspace, q_abs_offset=None, causal=True, out_dtype=None):
+        return query.new_empty(query.shape, dtype=out_dtype or query.dtype)
+
+    @custom_op(f"{_NS}::paged_attention_out",
+               mutates_args=("out", "workspace", "key_cache", "value_cache"))
+    def _paged_attention_out(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, block_table: torch.Tensor,
+                             seq_lens: torch.Tensor, query_start_loc: torch.Tensor, max_query_len: int, max_seq_len: int,
+                             scale: float, out: torch.Tensor, workspace: Optional[torch.Tensor],
+                             q_abs_offset: Optional[torch.Tensor] = None, causal: bool = True,
+                             new_key: Optional[torch.Tensor] = None, new_value: Optional[torch.Tensor] = None,
+                             slot_mapping: Optional[torch.Tensor] = None) -> None:
+        """The backend's step: attention into ``out`` (the model dtype), with
+        the step's K/V written to the cache first when new_key / new_value /
+        slot_mapping are given (the caches are in-place arguments for that)."""
+        need = workspace_size(seq_lens.shape[0], query.shape[0], query.shape[1], key_cache.shape[1],
+                              max_query_len, max_seq_len)
+        _check(workspace is None or workspace.numel() * workspace.element_size() >= need,
+               f"paged_attention_out: workspace needs {need} bytes")
+        paged_attention(query, key_cache, value_cache, block_table, seq_lens, query_start_loc, max_query_len,
+                        max_seq_len, scale, out=out, workspace=workspace, q_abs_offset=q_abs_offset,
+                        causal=causal, new_key=new_key, new_value=new_value, slot_mapping=slot_mapping)
+
+    @_paged_attention_out.register_fake
+    def _(query, key_cache, value_cache, block_table, seq_lens, query_start_loc, max_query_len, max_seq_len,
+          scale, out, workspace, q_abs_offset=None, causal=True, new_key=None, new_value=None,
+          slot_mapping=None):
+        return None
+
+
+TORCH_OPS = ("quantize_q8_0", "reshape_and_cache_q8", "gather_paged_kv_q8", "gather_paged_kv_q8_out",
+             "forward", "forward_paged_direct", "reshape_and_cache_q8_kv", "rope_and_cache_q8_kv",
+             "gather_paged_kv_q8q8", "paged_attention", "paged_attention_out")
+
 _load()
+if not hasattr(torch.ops, _NS) or not hasattr(getattr(torch.ops, _NS), "paged_attention"):
+    _register_torch_ops()
