@@ -210,6 +210,53 @@ def prefix_chunk_times(dev) -> dict:
     return res
 
 
+def gather_rates(dev) -> dict:
+    """The standalone gathers at cfg2's shape (32 sequences, contexts
+    U[2048, 16384], 8 kv-heads, block_size 16, permuted block tables, Sk the
+    longest context rounded up to 32): the reference's contract (AoS Q8_0 K
+    rows + fp16 V rows -> contiguous [B, Hkv, Sk, row],
+    extension/gfx906_fa_gather.cu:190-357) and the planar Q8 K+V planes ->
+    AoS Q8_0 rows.  Algorithmic bytes: the valid rows read, the K rows of
+    valid tokens and every V row (zeroed past seq_len) written, the block
+    table read."""
+    import numpy as np
+    import torch
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+    sl, _, _, Hkv, _ = W.cfg_shape("cfg2")
+    sl = np.asarray(sl, np.int32)
+    B, bs = len(sl), 16
+    rng = np.random.default_rng(3)
+    bt, nb = W.make_block_table(rng, sl, bs)
+    Sk = (int(sl.max()) + 31) // 32 * 32
+    M = bt.shape[1]
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    kc = torch.randint(0, 256, (nb, bs, Hkv, 136), dtype=torch.uint8, device=dev, generator=g)
+    vc = torch.randn((nb, bs, Hkv, 128), dtype=torch.float16, device=dev, generator=g)
+    btt = torch.from_numpy(bt).to(dev)
+    slt = torch.from_numpy(sl).to(dev)
+    ko = torch.empty((B, Hkv, Sk, 136), dtype=torch.uint8, device=dev)
+    vo = torch.empty((B, Hkv, Sk, 128), dtype=torch.float16, device=dev)
+    valid = int(np.minimum(sl, Sk).astype(np.int64).sum())
+    ref_bytes = valid * Hkv * (136 + 256) + valid * Hkv * 136 + B * Hkv * Sk * 256 + B * M * 4
+    ms_ref = timed(lambda: gfx906_fa.gather_paged_kv_q8(kc, vc, btt, slt, Sk, k_out=ko, v_out=vo), 20, 5)
+    del kc, vc
+    cache = torch.randint(0, 256, (nb, 2, Hkv, bs // 16 * 2176), dtype=torch.uint8, device=dev, generator=g)
+    vq = torch.empty((B, Hkv, Sk, 136), dtype=torch.uint8, device=dev)
+    pl_bytes = valid * Hkv * 272 + valid * Hkv * 136 + B * Hkv * Sk * 136 + B * M * 4
+    ms_pl = timed(lambda: gfx906_fa.gather_paged_kv_q8q8(cache[:, 0], cache[:, 1], btt, slt, Sk,
+                                                          k_out=ko, v_out=vq), 20, 5)
+    del cache, ko, vo, vq
+    torch.cuda.empty_cache()
+    gbs = lambda n, ms: round(n / (ms * 1e-3) / 1e9, 1)  # noqa: E731
+    return {"workload": f"cfg2 shape: {B} seqs, {valid} tokens, {Hkv} kv-heads, Sk {Sk}",
+            "reference_contract": {"us": round(ms_ref * 1e3, 1), "bytes": ref_bytes, "gbs": gbs(ref_bytes, ms_ref),
+                                   "frac_of_hbm_peak": round(ref_bytes / (ms_ref * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "planar_to_aos_q8": {"us": round(ms_pl * 1e3, 1), "bytes": pl_bytes, "gbs": gbs(pl_bytes, ms_pl),
+                                 "frac_of_hbm_peak": round(pl_bytes / (ms_pl * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+
+
 def _attn_fn(b, out, ws):
     import gfx906_fa
     kp, vp = b.planes()
@@ -498,7 +545,8 @@ def main() -> int:
     if graph is not None:
         res["next_rows"] = {"graph_replay": graph,
                             "output_epilogue": output_epilogue_ms(dev),
-                            "prefix_chunks": prefix_chunk_times(dev)}
+                            "prefix_chunks": prefix_chunk_times(dev),
+                            "gather": gather_rates(dev)}
 
     if args.calib_copy_mib:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE

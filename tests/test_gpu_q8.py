@@ -212,6 +212,23 @@ def test_gather_stress_and_edges(vq8):
     _gather_case(64, 16, 4, 128, bt, np.minimum(sl + 60, 200), 192, vq8, 3)  # Sk > M*bs
 
 
+@pytest.mark.parametrize("bs", [8, 32])
+@pytest.mark.parametrize("vq8", [False, True])
+def test_gather_block_sizes(vq8, bs):
+    """Both word paths of the row gather: block_size 8 takes the per-word
+    kernel (8-byte words), 32 the 16-byte slab kernel (a 16-token slab inside
+    one page); seq_lens that end mid-slab on odd token counts (an 8-byte K
+    tail), -1 pages, seq_len 0."""
+    need_gpu()
+    announce(f"gather block_size={bs} vq8={vq8}")
+    rng = np.random.default_rng(7 + bs)
+    M = 256 // bs
+    bt = rng.integers(0, 40, (6, M))
+    bt[4, 1] = -1
+    sl = np.array([0, 17, 255, 33, 200, 129])
+    _gather_case(40, bs, 3, 128, bt, sl, 256, vq8, 4)
+
+
 @pytest.mark.parametrize("bs", [16, 64])
 def test_gather_planar(bs):
     need_gpu()
@@ -231,6 +248,35 @@ def test_gather_planar(bs):
     ke, ve = O.gather_paged_kv_q8_aos(ka, va, bt, sl, Sk, k_out=np.full(tuple(kbuf.shape), 0xAB, np.uint8))
     assert np.array_equal(ko.cpu().numpy(), ke)
     assert np.array_equal(vo.cpu().numpy(), ve)
+
+
+def test_gather_planar_unaligned_outputs():
+    """The planar gather's per-word kernel, taken for outputs that are not
+    16-byte aligned (here 4 bytes past an allocation), through the C ABI."""
+    need_gpu()
+    announce("gather planar unaligned outputs")
+    rng = np.random.default_rng(12)
+    NB, Hkv, B, M, bs = 10, 2, 3, 2, 32
+    bt = rng.integers(0, NB, (B, M)).astype(np.int32)
+    bt[2, 1] = -1
+    sl = np.array([5, 64, 40], np.int32)
+    Sk = 64
+    cache = torch.from_numpy(rng.integers(0, 256, (NB, 2, Hkv, bs // 16 * 2176), dtype=np.uint8)).to(DEV)
+    n = B * Hkv * Sk * 136
+    kraw = torch.full((n + 4,), 0xAB, dtype=torch.uint8, device=DEV)
+    vraw = torch.full((n + 4,), 0xCD, dtype=torch.uint8, device=DEV)
+    btt, slt = torch.from_numpy(bt).to(DEV), torch.from_numpy(sl).to(DEV)
+    kp, vp = cache[:, 0], cache[:, 1]
+    err = gfx906_fa.lib().gfx906_fa_amd_gather_planar(
+        kp.data_ptr(), vp.data_ptr(), btt.data_ptr(), slt.data_ptr(), kraw.data_ptr() + 4, vraw.data_ptr() + 4,
+        B, Hkv, Sk, 128, bs, M, kp.stride(0), kp.stride(1), stream_ptr())
+    assert err == 0
+    torch.cuda.synchronize()
+    ka, va = O.planar_to_aos(cache.cpu().numpy())
+    ke, ve = O.gather_paged_kv_q8_aos(ka, va, bt, sl, Sk, k_out=np.full((B, Hkv, Sk, 136), 0xAB, np.uint8))
+    assert np.array_equal(kraw[4:].cpu().numpy().reshape(B, Hkv, Sk, 136), ke)
+    assert np.array_equal(vraw[4:].cpu().numpy().reshape(B, Hkv, Sk, 136), ve)
+    assert int(kraw[:4].sum()) == 4 * 0xAB and int(vraw[:4].sum()) == 4 * 0xCD
 
 
 def test_roundtrip_write_gather_dequant():
