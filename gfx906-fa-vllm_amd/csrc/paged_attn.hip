@@ -138,7 +138,9 @@ __device__ __forceinline__ void store_out(void *out, int64_t off, float v) {
 
 // Raw operand registers for one 16-token sub-page.
 struct SubPage {
-    u32x4 kq[2], ks[2], vq[2], vs[2];
+    u32x4 kq[2];
+    u32x2 ks;  // the four block scales of the lane's token i16
+    u32x4 vq[2], vs[2];
 };
 
 // Per-lane byte offsets of a lane's operands inside a 2176-byte sub-page.
@@ -149,7 +151,7 @@ struct LaneOffsets {
 __device__ __forceinline__ LaneOffsets lane_offsets(int i16, int g) {
     LaneOffsets o;
     o.kq = (4 * i16 + g) * 16;          // K ints of token i16, group g: +0 and +1024
-    o.ks = SCALE_OFF + 32 * g;          // K scales of tokens 4g..4g+3
+    o.ks = SCALE_OFF + 8 * i16;         // K scales of token i16, blocks 0..3
     o.vq = (16 * g + i16) * 16;         // V ints, d = 16m + i16, tokens 4g..4g+3: +0 and +1024
     o.vs = SCALE_OFF + 32 * g;          // V scales of tokens 4g..4g+3
     return o;
@@ -161,7 +163,7 @@ template <bool NT>
 __device__ __forceinline__ void load_subpage(SubPage &sp, const uint8_t *kb, const uint8_t *vb,
                                              const LaneOffsets &lo) {
     const u32x4 *k0 = reinterpret_cast<const u32x4 *>(kb + lo.kq);
-    const u32x4 *ks = reinterpret_cast<const u32x4 *>(kb + lo.ks);
+    const u32x2 *ks = reinterpret_cast<const u32x2 *>(kb + lo.ks);
     const u32x4 *v0 = reinterpret_cast<const u32x4 *>(vb + lo.vq);
     const u32x4 *vs = reinterpret_cast<const u32x4 *>(vb + lo.vs);
     if constexpr (NT) {  // each KV byte is read once: keep it out of the caches
@@ -175,8 +177,7 @@ __device__ __forceinline__ void load_subpage(SubPage &sp, const uint8_t *kb, con
         sp.vq[0] = v0[0];
         sp.vq[1] = v0[64];
     }
-    sp.ks[0] = ks[0];
-    sp.ks[1] = ks[1];
+    sp.ks = ks[0];
     sp.vs[0] = vs[0];
     sp.vs[1] = vs[1];
 }
@@ -214,7 +215,9 @@ __device__ __forceinline__ float4_t mfma16k16(half4_t a, half4_t b, float4_t c) 
 }
 
 // One 16-token sub-page starting at tok0.
-//   QK: 4 x mfma 16x16x32 (one per Q8 block), K scales on the fp32 products.
+//   QK: 4 x mfma 16x16x32 (one per Q8 block) in one accumulator chain over
+//       K^ = fp16(q * d_k): each lane dequantizes the 32 values of its own
+//       token i16 once (v_pk_mul_f16, one rounding), for all row groups.
 //   PV: 8 x mfma 16x16x16 (one per 16 d); lane (i, g) feeds tokens 4g..4g+3,
 //       the same tokens its S^T fragment holds, so P needs no shuffles.
 // mask (wave-uniform): apply kv_end and the per-row causal bounds lim[rg].
@@ -224,21 +227,20 @@ __device__ __forceinline__ void attend_subpage(WaveAcc<NRG> &acc, const SubPage 
                                                const int (&lim)[NRG], float c, int g, bool mask) {
     half8_t ka[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) ka[b] = i8x8_to_half8(dw(sp.kq, 2 * b), dw(sp.kq, 2 * b + 1));
+    for (int b = 0; b < 4; ++b) {
+        const uint32_t sw = sp.ks[b >> 1];
+        const half_t d = __builtin_bit_cast(half2_t, sw)[b & 1];
+        const half8_t dd = {d, d, d, d, d, d, d, d};
+        ka[b] = i8x8_to_half8(dw(sp.kq, 2 * b), dw(sp.kq, 2 * b + 1)) * dd;
+    }
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
-        float4_t cb[4];
+        float4_t sacc = mfma16(ka[0], qf[rg][0], float4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int b = 0; b < 4; ++b) cb[b] = mfma16(ka[b], qf[rg][b], float4_t{0.f, 0.f, 0.f, 0.f});
+        for (int b = 1; b < 4; ++b) sacc = mfma16(ka[b], qf[rg][b], sacc);
         float sv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // K scales of token 4g+i: blocks (0,1), (2,3)
-            const uint32_t s01 = dw(sp.ks, 2 * i), s23 = dw(sp.ks, 2 * i + 1);
-            float v = cb[0][i] * hlo(s01);
-            v = fmaf(cb[1][i], hhi(s01), v);
-            v = fmaf(cb[2][i], hlo(s23), v);
-            sv[i] = fmaf(cb[3][i], hhi(s23), v);
-        }
+        for (int i = 0; i < 4; ++i) sv[i] = sacc[i];  // token 4g + i
         if (mask) {  // uniform: only partial / causal-diagonal sub-pages
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
