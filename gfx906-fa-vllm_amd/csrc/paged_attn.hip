@@ -12,8 +12,9 @@
 //   O^T[16 d x 16 rows]  += V^T[16 d x 16 tok] . P'^T[16 tok x 16 rows]
 //       one v_mfma_f32_16x16x16_f16 per 16 d
 // Lane l = 16*g + i: row i (column of S^T / O^T), token group / d group g.
-// K int8 values enter the MFMA exactly (int8 -> fp16 is exact) and the fp16
-// block scale multiplies the fp32 product.  V int8 values also enter exactly;
+// A lane dequantizes the K values of its own token to fp16 once per sub-page
+// (K^ = q * d_k, one rounding), and the four MFMAs of the row group
+// accumulate into one chain.  V int8 values enter the MFMA exactly;
 // the V scale d_v[t][b] is folded into P (P'_b[t] = p[t] * d_v[t][b], fp16)
 // for the MFMAs of d-block b.  Softmax statistics and O accumulate in fp32.
 //
