@@ -555,9 +555,9 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         // sl - n_q .. sl - 1, input rows q0 ..) that lie in a piece's
         // sub-pages are quantized and stored by the wave that will stream
         // their sub-page (wave (js - a) % DEC_NW takes sub-page js of piece
-        // [a, b)), so each new (token, kv-head) is written once, by the only
-        // wave that reads it in this launch, and that wave's later loads
-        // follow its own stores in program order.
+        // [a, b)), so each new (token, kv-head) is written by the wave that
+        // reads it in this launch (by both, in the two-chunk mode), and that
+        // wave's later loads follow its own stores in program order.
         int64_t uu = u0, Pw = Ps;
         int sw = s;
         SegInfo sv = si;
@@ -567,8 +567,12 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
             const int a = (int)(off - (int64_t)hh * sv.nsub);
             const int b = (int)min((int64_t)sv.nsub, a + (u1 - uu));
             const int lo = sv.sl - sv.nq;
+            // two row chunks at once (see rows_pass below): sub-page js is
+            // streamed by the two waves with (js - a) % 2 == wv % 2, and both
+            // write its new tokens (the same bytes), each before its own loads
+            const bool dual = CHUNK && sv.nq * p.G > R;
             for (int js = max(a, lo >> 4); js < b; ++js) {  // uniform
-                if (((js - a) & (DEC_NW - 1)) != wv) continue;
+                if (dual ? (((js - a) & 1) != (wv & 1)) : (((js - a) & (DEC_NW - 1)) != wv)) continue;
                 const int t_hi = min(16 * js + 16, sv.sl);
                 for (int pos = max(16 * js, lo); pos < t_hi; ++pos)
                     write_new_token<QDT>(p, hh, sv.q0 + (pos - lo), lane);
@@ -601,9 +605,15 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         const int nrows = si.nq * p.G;
 
         // CHUNK: rows beyond one tile (up to 64: a verify step of 6 tokens at
-        // 6 q-heads per kv-head is 36 rows) are taken R at a time, each chunk
-        // streaming the piece's keys again; otherwise one pass
-        auto rows_pass = [&](int rc) {
+        // 6 q-heads per kv-head is 36 rows) are taken in two R-row chunks at
+        // once: waves 0, 1 hold rows 0..R-1 and waves 2, 3 rows R..2R-1, each
+        // pair interleaving the piece's sub-pages the same way, so a sub-page
+        // is fetched by two waves of the CU close together and the second
+        // fetch is served by the caches, not HBM.  Otherwise the four waves
+        // interleave over the piece for one row tile.
+        // rc: this wave's first row; j0 / jstep: its sub-pages of the piece;
+        // wpc: waves per chunk (their states are merged).
+        auto rows_pass = [&](int rc, int j0, int jstep, int wpc) {
         half8_t qf[NRG][4];
         int lim[NRG];
         load_rows<NRG, QDT>(p, h, si.q0, nrows, rc, si.sl, si.qa, i16, g, qf, lim);
@@ -611,8 +621,8 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         acc_init(acc);
         stream_range<NRG, GFA_DEC_NT != 0, DecCfg<NRG>::depth>(acc, p, s, h, 16 * a,
                                                                  min(16 * b, si.kv_lim), qf, lim,
-                                                                 lane, i16, g, wv, DEC_NW);
-        // ---- merge the four waves' states in LDS ---------------------------
+                                                                 lane, i16, g, j0, jstep);
+        // ---- merge the chunk's waves' states in LDS ------------------------
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
             const float l = xrow_sum(acc.l[rg]);
@@ -628,18 +638,18 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         __syncthreads();
         const bool whole = a == 0 && b == si.nsub;
         const int slot = 2 * w + (first ? 0 : 1);
-        const int rows_c = CHUNK ? min(R, nrows - rc) : nrows;
+        const int rows_c = CHUNK ? nrows : min(nrows, R);
         for (int it = threadIdx.x; it < rows_c * 32; it += 64 * DEC_NW) {
-            const int rl = it >> 5, d0 = (it & 31) * 4;
-            const int r = rc + rl;
+            const int r = it >> 5, d0 = (it & 31) * 4;
+            const int ch = CHUNK ? r / R : 0;   // the row's chunk: waves ch*wpc .. ch*wpc + wpc - 1
+            const int rl = r - ch * R;          // its row inside the chunk
+            const int k0 = ch * wpc;
             float mx = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < DEC_NW; ++k) mx = fmaxf(mx, sm_m[k][rl]);
+            for (int k = k0; k < k0 + wpc; ++k) mx = fmaxf(mx, sm_m[k][rl]);
             const float ms = mx == -INFINITY ? 0.0f : mx;
             float l = 0.f;
             float4_t o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int k = 0; k < DEC_NW; ++k) {
+            for (int k = k0; k < k0 + wpc; ++k) {
                 const float wk = __builtin_amdgcn_exp2f(sm_m[k][rl] - ms);
                 l = fmaf(sm_l[k][rl], wk, l);
                 o += *reinterpret_cast<const float4_t *>(&sm_o[k][rl][d0]) * wk;
@@ -660,12 +670,13 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
                 }
             }
         }
-        __syncthreads();  // LDS reused by the next row chunk / piece
+        __syncthreads();  // LDS reused by the next piece
         };
-        if constexpr (CHUNK) {
-            for (int rc = 0; rc < nrows; rc += R) rows_pass(rc);
+        static_assert(DEC_NW == 4 && DEC_CHUNK_ROWS <= 2 * 32, "two row chunks of two waves each");
+        if (CHUNK && nrows > R) {  // uniform: rows R..nrows-1 (nrows <= 2R) in the second chunk
+            rows_pass(R * (wv >> 1), wv & 1, 2, DEC_NW / 2);
         } else {
-            rows_pass(0);
+            rows_pass(0, wv, DEC_NW, DEC_NW);
         }
         u += b - a;
         first = false;
