@@ -724,8 +724,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     float m = -INFINITY, l = 0.f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
     // group `sub` merges pieces wf + sub, wf + sub + 8, ... in order; the loads
-    // of four of them are issued before they are merged (in flight together)
-    constexpr int CU = 4;
+    // of CU of them are issued before they are merged (in flight together)
+#ifndef GFA_COMB_CU
+#define GFA_COMB_CU 8
+#endif
+    constexpr int CU = GFA_COMB_CU;
     for (int k0 = wf + sub; k0 <= wl; k0 += 8 * CU) {
         float2_t mlk[CU];
         float4_t ok[CU];
