@@ -1002,9 +1002,6 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
         // cbase + 64 + i).  Tile t sits in ring slot t % PF_PDEPTH from its
         // fetch until its dequant, one iteration before the consumers read it.
         const int wsp = w - PF_CWAVES;
-#ifdef GFA_PF_PRIO
-        __builtin_amdgcn_s_setprio(GFA_PF_PRIO);
-#endif
         const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
         const int bs = p.block_size;
         const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
