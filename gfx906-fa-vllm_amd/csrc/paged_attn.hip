@@ -313,8 +313,9 @@ __device__ __forceinline__ void load_rows(const AttnParams &p, int h, int q0, in
 // Streams the keys [wb, we) (wb a multiple of 16) through the wave, two
 // sub-pages per k-step, with register ping-pong prefetch one k-step ahead.
 // Page ids come from a lane-distributed copy of the block table (lane i holds
-// the page of sub-page 64*chunk + i), refreshed one chunk ahead, so no load in
-// the loop depends on another load.
+// the page of sub-page 64*chunk + i, and the sub-page's index in that page),
+// refreshed one chunk ahead, so no load in the loop depends on another load
+// and a sub-page's address is scalar arithmetic (no division per sub-page).
 // j0 / jstep: the wave takes sub-pages j0, j0 + jstep, ... of the range (the
 // waves of a workgroup interleave over one range).
 template <int NRG, bool NT, int DEPTH>
@@ -328,13 +329,17 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
     const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
     const uint8_t *kbase = p.kc + (int64_t)h * p.chs;
     const uint8_t *vbase = p.vc + (int64_t)h * p.chs;
-    const int bs = p.block_size;
-    auto load_pg = [&](int chunk) -> int {
+    const int spp = p.block_size >> 4;  // sub-pages per page
+    auto load_pg = [&](int chunk, int &spi) -> int {
         const int j = 64 * chunk + lane;
-        return j < nsub ? btrow[(wb + 16 * (j0 + jstep * j)) / bs] : 0;
+        const int sp = (wb >> 4) + j0 + jstep * j;  // the sub-page's index in the sequence
+        const int pi = sp / spp;
+        spi = sp - pi * spp;
+        return j < nsub ? btrow[pi] : 0;
     };
-    int pg_cur = load_pg(0);
-    int pg_nxt = nsub > 64 ? load_pg(1) : 0;
+    int ps_cur = 0, ps_nxt = 0;
+    int pg_cur = load_pg(0, ps_cur);
+    int pg_nxt = nsub > 64 ? load_pg(1, ps_nxt) : 0;
     int chunk = 0;
     // smallest causal bound over the wave's real rows: a k-step entirely below
     // it (and below we) needs no mask
@@ -354,11 +359,12 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
             if ((j >> 6) != chunk) {  // advance the page-id window (uniform)
                 chunk = j >> 6;
                 pg_cur = pg_nxt;
-                pg_nxt = 64 * (chunk + 1) < nsub ? load_pg(chunk + 1) : 0;
+                ps_cur = ps_nxt;
+                pg_nxt = 64 * (chunk + 1) < nsub ? load_pg(chunk + 1, ps_nxt) : 0;
             }
-            const int tb = wb + 16 * (j0 + jstep * j);
             const int64_t page = __builtin_amdgcn_readlane(pg_cur, j & 63);
-            const int64_t off = page * p.cbs + (int64_t)((tb % bs) >> 4) * SUBPAGE_BYTES;
+            const int spi = __builtin_amdgcn_readlane(ps_cur, j & 63);
+            const int64_t off = page * p.cbs + (int64_t)spi * SUBPAGE_BYTES;
             load_subpage<NT>(sp, kbase + off, vbase + off, lo);
         }
     };
