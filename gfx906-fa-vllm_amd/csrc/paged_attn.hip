@@ -513,19 +513,39 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     const int B = p.num_seqs, Hkv = p.Hkv;
     const int w = blockIdx.x;
 
+    // Batches of up to 64 sequences (uniform): lane i loads sequence i's
+    // metadata once, and the plan, the segment search and the segment's own
+    // fields all come from those registers - one memory round trip where the
+    // general path below takes three before the first K/V load.
+    const bool small = B <= 64;
+    SegInfo lsi = seg_info(p, small ? min(lane, B - 1) : 0);
+    const int ln = small && lane < B ? lsi.nsub : 0;
+    const int lincl = wave_incl_scan(ln, lane);
     int64_t U;
     int nwg;
-    dec_total(p, lane, U, nwg);
+    if (small) {
+        const int64_t tot = __shfl(lincl, 63);
+        const int nseg = __builtin_popcountll(__ballot(ln > 0));
+        U = uniform64(tot * Hkv);
+        const int64_t want = max(U / DEC_MIN_UNITS, (int64_t)nseg * Hkv);
+        nwg = (int)max((int64_t)1, min((int64_t)p.nwg, want));
+    } else {
+        dec_total(p, lane, U, nwg);
+    }
     if (w == 0 && wv == 0) {
         // publish the plan for attn_combine_kernel: U, nwg, per-sequence
         // exclusive prefix of decode sub-pages
-        int64_t run = 0;
-        for (int base = 0; base < B; base += 64) {
-            const int sj = base + lane;
-            const int n = sj < B ? seg_info(p, sj).nsub : 0;
-            const int incl = wave_incl_scan(n, lane);
-            if (sj < B) p.ws_pre[sj] = (int)run + incl - n;
-            run += __shfl(incl, 63);
+        if (small) {
+            if (lane < B) p.ws_pre[lane] = lincl - ln;
+        } else {
+            int64_t run = 0;
+            for (int base = 0; base < B; base += 64) {
+                const int sj = base + lane;
+                const int n = sj < B ? seg_info(p, sj).nsub : 0;
+                const int incl = wave_incl_scan(n, lane);
+                if (sj < B) p.ws_pre[sj] = (int)run + incl - n;
+                run += __shfl(incl, 63);
+            }
         }
         if (lane == 0) {
             p.ws_hdr[0] = U;
@@ -537,23 +557,36 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     // locate the sequence holding u0 (Ps = sub-pages of the sequences before s)
     int s = 0;
     int64_t Ps = 0;
-    for (int base = 0; base < B; base += 64) {
-        const int si = base + lane;
-        const int n = si < B ? seg_info(p, si).nsub : 0;
-        const int incl = wave_incl_scan(n, lane);
-        const int ctot = __shfl(incl, 63);
-        if ((Ps + ctot) * Hkv > u0) {
-            const uint64_t bal = __ballot((Ps + incl) * Hkv > u0);
-            const int i = __builtin_ctzll(bal);
-            s = base + i;
-            Ps += __shfl(incl - n, i);
-            break;
+    SegInfo si;
+    if (small) {
+        const uint64_t bal = __ballot((int64_t)lincl * Hkv > u0);  // non-empty: u0 < U
+        s = __builtin_ctzll(bal);
+        Ps = __builtin_amdgcn_readlane(lincl - ln, s);
+        si.q0 = __builtin_amdgcn_readlane(lsi.q0, s);
+        si.nq = __builtin_amdgcn_readlane(lsi.nq, s);
+        si.sl = __builtin_amdgcn_readlane(lsi.sl, s);
+        si.qa = __builtin_amdgcn_readlane(lsi.qa, s);
+        si.kv_lim = __builtin_amdgcn_readlane(lsi.kv_lim, s);
+        si.nsub = __builtin_amdgcn_readlane(lsi.nsub, s);
+    } else {
+        for (int base = 0; base < B; base += 64) {
+            const int sidx = base + lane;
+            const int n = sidx < B ? seg_info(p, sidx).nsub : 0;
+            const int incl = wave_incl_scan(n, lane);
+            const int ctot = __shfl(incl, 63);
+            if ((Ps + ctot) * Hkv > u0) {
+                const uint64_t bal = __ballot((Ps + incl) * Hkv > u0);
+                const int i = __builtin_ctzll(bal);
+                s = base + i;
+                Ps += __shfl(incl - n, i);
+                break;
+            }
+            Ps += ctot;
         }
-        Ps += ctot;
+        s = __builtin_amdgcn_readfirstlane(s);
+        Ps = uniform64(Ps);
+        si = seg_info(p, s);
     }
-    s = __builtin_amdgcn_readfirstlane(s);
-    Ps = uniform64(Ps);
-    SegInfo si = seg_info(p, s);
 
     if (p.new_k) {
         // Fused cache write, before any streaming: the walk of the main loop
