@@ -454,6 +454,22 @@ def test_decode_many_short_sequences():
     _run_and_check(b)
 
 
+@pytest.mark.parametrize("nseq", [63, 64, 65])
+def test_decode_batch_size_boundary(nseq):
+    """Batches on both sides of 64 sequences (the decode kernel locates its
+    segment from one per-lane metadata load up to 64, and scans the
+    sequences beyond): decodes and 5-token verifies of 1..2500 tokens with
+    prefill chunks (no decode work) and empty queries interleaved, so
+    segments without decode sub-pages sit between split ones."""
+    need_gpu()
+    rng = np.random.default_rng(40 + nseq)
+    kinds = rng.integers(0, 10, nseq)
+    ql = [0 if k == 0 else (70 if k == 1 else (5 if k < 5 else 1)) for k in kinds]
+    sl = [q + int(c) for q, c in zip(ql, rng.integers(1, 2500, nseq))]
+    b = W.build_batch(sl, ql, 12, 2, seed=40 + nseq)
+    _run_and_check(b)
+
+
 def test_mixed_many_chunks():
     """Varlen mix of 40 prefill chunks (n_q 2..300, causal within each, prior
     context 0..3000) and 100 decode sequences in one call."""
