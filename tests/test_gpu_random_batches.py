@@ -1,0 +1,47 @@
+"""GPU: seeded random varlen batches against the float64 oracle.
+
+Each case draws a batch the way a vLLM scheduler step can look: up to 100
+sequences, each an empty query, a decode token, a short speculative-verify
+block or a prefill chunk on a cached prefix, over a shuffled paged cache
+with block sizes 16..64 and GQA shapes from 1 to 16 query heads per kv-head.
+One call covers both decode row classes, the tiled prefill kernel (split
+over the keys where its plan decides so) and the segment search on both
+sides of 64 sequences.  The cases are fixed by their seeds; the tolerance is
+the one in tests/test_gpu_attention.py (reference test strategy:
+tests/test_fa_mixed_batch.py, tests/test_decode_batch.py)."""
+import numpy as np
+import pytest
+import torch
+
+import gfx906_fa_workloads as W
+from gpu_common import announce, assert_close, batch_oracle, need_gpu, to_np_f32
+
+pytestmark = pytest.mark.gpu
+
+HEADS = [(8, 1), (12, 2), (48, 8), (6, 1), (64, 4), (16, 16), (32, 8)]
+
+
+def _draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    nseq = int(rng.choice([1, 3, 8, 31, 63, 64, 65, 100])) if seed % 3 else int(rng.integers(1, 101))
+    hq, hkv = HEADS[seed % len(HEADS)]
+    bs = int(rng.choice([16, 32, 64]))
+    dt = "bf16" if seed % 2 else "f16"
+    kind = rng.choice(4, size=nseq, p=[0.05, 0.55, 0.3, 0.1])
+    ql = np.where(kind == 0, 0, np.where(kind == 1, 1, np.where(kind == 2, rng.integers(2, 7, nseq),
+                                                                 rng.integers(7, 121, nseq))))
+    ctx = rng.integers(0, 3000, nseq)
+    sl = [int(q + c) if q + c > 0 else 1 for q, c in zip(ql, ctx)]
+    return sl, [int(q) for q in ql], hq, hkv, bs, dt
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_batch_matches_oracle(seed):
+    need_gpu()
+    sl, ql, hq, hkv, bs, dt = _draw(seed)
+    announce(f"random batch seed={seed} B={len(sl)} heads={hq}/{hkv} bs={bs} {dt} "
+             f"max_q={max(ql)} max_k={max(sl)}")
+    b = W.build_batch(sl, ql, hq, hkv, block_size=bs, dtype=dt, seed=2000 + seed)
+    out = W.attention(b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(to_np_f32(out), batch_oracle(b))
