@@ -94,6 +94,16 @@ struct AttnParams {
     int pf_slots_max;   // partial slots per kv head
     int *pf_split;      // split row tiles: (sequence, row tile, first slot, pieces) each
     float *pf_ml, *pf_o;  // partials: [slot][Hkv][PF_ROWS] x (m, l) and x 128
+    // Dequantized tile images (work-list launches only; nullptr: none): the
+    // fp16 K^ and V^T of 64-key tile kt of prefill sequence s for kv-head h,
+    // byte for byte the prefill kernel's LDS stages, at image
+    // (pf_tbase[s] + kt) * Hkv + h of pf_tiles, written once per call by
+    // prefill_tiles_kernel when every image fits pf_tiles_cap bytes (the plan
+    // kernel sets pf_count[2]); the prefill workgroups then copy them into
+    // LDS instead of dequantizing every tile themselves.
+    uint8_t *pf_tiles;
+    int *pf_tbase;      // per sequence (num_seqs + 1): first image tile
+    int64_t pf_tiles_cap;
     // Fused cache write of the step's new tokens (decode kernels only; nullptr:
     // none).  Row qsl[s] + j of new_k / new_v (the query dtype) holds the key /
     // value of position seq_lens[s] - n_q + j, written at slot new_slot[row].
@@ -875,6 +885,18 @@ constexpr int PF_KPITCH = 272;
 constexpr int PF_VPITCH = 2 * PF_TK + 16;
 constexpr int PF_KBYTES = PF_TK * PF_KPITCH;
 constexpr int PF_VBYTES = 128 * PF_VPITCH;
+constexpr int PF_IMG_BYTES = PF_KBYTES + PF_VBYTES;  // one tile image: K^ stage, then V^T stage
+constexpr int PF_NSTAGE = 3;                           // LDS stages of K^ and of V^T (tile t: stage t % 3)
+#ifndef GFA_PF_IMG_REUSE
+#define GFA_PF_IMG_REUSE 32
+#endif
+constexpr int PF_IMG_REUSE = GFA_PF_IMG_REUSE;         // reads per tile image, on average, at least
+// a tile image is copied into LDS as four equal shares, one per producer
+// wave, each 4 x 1 KB plus a partial 1 KB row (64 lanes x 16 bytes per copy)
+constexpr int PF_KSHARE = PF_KBYTES / PF_PWAVES, PF_VSHARE = PF_VBYTES / PF_PWAVES;
+static_assert(PF_KSHARE % 16 == 0 && PF_VSHARE % 16 == 0 && PF_KSHARE / 1024 == 4 && PF_VSHARE / 1024 == 4 &&
+                  PF_KSHARE % 1024 != 0 && PF_VSHARE % 1024 != 0,
+              "five copies per wave and stage");
 
 typedef float float16v_t __attribute__((ext_vector_type(16)));
 typedef uint64_t u64x8_t __attribute__((ext_vector_type(8)));
@@ -992,13 +1014,9 @@ __device__ __forceinline__ void pf_dequant_v(const PfRaw &r, uint8_t *vst, int s
 template <int QDT, int ODT, bool VF16, bool MASK>
 __global__ __launch_bounds__(64 * PF_WAVES)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p) {
-    // two LDS stages of K^ and of V^, each a distinct object: the compiler
-    // can then prove that the stores into one and the reads of the other are
-    // independent
-    __shared__ __attribute__((aligned(16))) uint8_t ldsk0[PF_KBYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t ldsk1[PF_KBYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t ldsv0[PF_VBYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t ldsv1[PF_VBYTES];
+    // three LDS stages of K^ and of V^T (tile t in stage t % 3)
+    __shared__ __attribute__((aligned(16))) uint8_t ldsk[PF_NSTAGE * PF_KBYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsv[PF_NSTAGE * PF_VBYTES];
     const int Hkv = p.Hkv;
     const int h = blockIdx.x % Hkv;
     int s, rt, kt0 = 0, kt1 = INT32_MAX, slot = -1;
@@ -1041,6 +1059,51 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
         // cbase + 64 + i).  Tile t sits in ring slot t % PF_PDEPTH from its
         // fetch until its dequant, one iteration before the consumers read it.
         const int wsp = w - PF_CWAVES;
+        if (p.pf_tiles != nullptr && p.pf_count[2] != 0) {  // uniform
+            // The tiles are dequantized images in the workspace.  Copy batch
+            // b (K^ of tile b/2 for even b, V^T for odd b) goes from the image
+            // straight into its LDS stage in half-step b - 4 and has landed by
+            // the end of half-step b - 1, before the barrier that opens the
+            // consumers' first read of it.  The stage it fills was last read
+            // in half-step b - 5 (tile b/2 - 3).  Each wave copies one quarter
+            // of a stage per batch: exactly five copies, so "batch h + 1 has
+            // landed" at the end of half-step h is vmcnt(15) (the three later
+            // batches may still be in flight), or vmcnt(0) near the end, where
+            // fewer batches follow.
+            const int64_t istride = (int64_t)Hkv * PF_IMG_BYTES;
+            const uint8_t *img0 = p.pf_tiles + ((int64_t)(p.pf_tbase[s] + ktb) * Hkv + h) * PF_IMG_BYTES;
+            auto copy = [&](int b) __attribute__((always_inline)) {
+                const int t = b >> 1;
+                if (t >= ntk) return;  // uniform
+                const bool isv = b & 1;
+                const int share = isv ? PF_VSHARE : PF_KSHARE;
+                const uint8_t *src = img0 + t * istride + (isv ? PF_KBYTES : 0) + wsp * share;
+                uint8_t *dst = (isv ? ldsv + (t % PF_NSTAGE) * PF_VBYTES : ldsk + (t % PF_NSTAGE) * PF_KBYTES) +
+                               wsp * share;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    __builtin_amdgcn_global_load_lds(src + i * 1024 + lane * 16,
+                                                     (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
+                if (16 * lane < share - 4096)  // the partial row
+                    __builtin_amdgcn_global_load_lds(src + 4096 + lane * 16,
+                                                     (__attribute__((address_space(3))) void *)(dst + 4096), 16, 0, 0);
+            };
+            // the end of half-step h (h = -1: before the first barrier)
+            auto landed = [&](int h) __attribute__((always_inline)) {
+                if (h + 4 < 2 * ntk) __builtin_amdgcn_s_waitcnt(0x0F7F);  // vmcnt(15)
+                else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+            };
+#pragma unroll
+            for (int b = 0; b < 4; ++b) copy(b);
+            landed(-1);
+            __syncthreads();
+            for (int hs = 0; hs <= 2 * ntk; ++hs) {  // half-steps 0 .. 2 ntk
+                copy(hs + 4);
+                landed(hs);
+                __syncthreads();
+            }
+            return;
+        }
         const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
         const int bs = p.block_size;
         const int last_sp = max((kv_end - 1) >> 4, 0);  // last sub-page with a valid key
@@ -1091,14 +1154,14 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
                 ready(pw1);
             }
         };
-        // dequantizes the K (or V) half of tile t (in the ring) into stage t & 1
-        auto dequant_k = [&](const PfRawT &rw, auto odd) __attribute__((always_inline)) {
-            uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
+        // dequantizes the K (or V) half of tile t (in the ring) into stage t % 3
+        auto dequant_k = [&](const PfRawT &rw, int t) __attribute__((always_inline)) {
+            uint8_t *kst = ldsk + (t % PF_NSTAGE) * PF_KBYTES;
             pf_dequant_k(rw.h[0], kst, wsp, lane, 0, p.pf_kmul);
             pf_dequant_k(rw.h[1], kst, wsp, lane, 1, p.pf_kmul);
         };
-        auto dequant_v = [&](const PfRawT &rw, auto odd, auto tail) __attribute__((always_inline)) {
-            uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
+        auto dequant_v = [&](const PfRawT &rw, int t, auto tail) __attribute__((always_inline)) {
+            uint8_t *vst = ldsv + (t % PF_NSTAGE) * PF_VBYTES;
             constexpr bool T = decltype(tail)::value;
             pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, 0);
             pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
@@ -1112,9 +1175,9 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
             ready(pw1);
 #pragma unroll
             for (int i = 0; i < PF_PDEPTH; ++i) fetch(ring[i], i);
-            dequant_k(ring[0], Even{});
-            if (ntk == 1) dequant_v(ring[0], Even{}, IsTail{});
-            else dequant_v(ring[0], Even{}, NoTail{});
+            dequant_k(ring[0], 0);
+            if (ntk == 1) dequant_v(ring[0], 0, IsTail{});
+            else dequant_v(ring[0], 0, NoTail{});
             fetch(ring[0], PF_PDEPTH);
         }
         __syncthreads();
@@ -1125,10 +1188,9 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
         // t + PF_PDEPTH.
         auto hstep = [&](int t, auto slot_c) __attribute__((always_inline)) {
             constexpr int SL = decltype(slot_c)::value;  // t % PF_PDEPTH
-            using StageOdd = std::integral_constant<bool, (SL & 1) != 0>;
-            dequant_k(ring[SL], StageOdd{});
+            dequant_k(ring[SL], t);
             __syncthreads();
-            dequant_v(ring[SL], StageOdd{}, NoTail{});
+            dequant_v(ring[SL], t, NoTail{});
             fetch(ring[SL], t + PF_PDEPTH);
             __syncthreads();
         };
@@ -1155,11 +1217,12 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
             if (rem >= 3) hstep(t + 2, S3{});
         }
         if (ntk >= 2) {  // tile ntk - 1 from slot (ntk - 1) % PF_PDEPTH
-            switch ((ntk - 1) % PF_PDEPTH) {
-            case 0: dequant_k(ring[0], Even{}); __syncthreads(); dequant_v(ring[0], Even{}, IsTail{}); break;
-            case 1: dequant_k(ring[1 % PF_PDEPTH], Odd{}); __syncthreads(); dequant_v(ring[1 % PF_PDEPTH], Odd{}, IsTail{}); break;
-            case 2: dequant_k(ring[2 % PF_PDEPTH], Even{}); __syncthreads(); dequant_v(ring[2 % PF_PDEPTH], Even{}, IsTail{}); break;
-            default: dequant_k(ring[3 % PF_PDEPTH], Odd{}); __syncthreads(); dequant_v(ring[3 % PF_PDEPTH], Odd{}, IsTail{}); break;
+            const int tl = ntk - 1;
+            switch (tl % PF_PDEPTH) {
+            case 0: dequant_k(ring[0], tl); __syncthreads(); dequant_v(ring[0], tl, IsTail{}); break;
+            case 1: dequant_k(ring[1 % PF_PDEPTH], tl); __syncthreads(); dequant_v(ring[1 % PF_PDEPTH], tl, IsTail{}); break;
+            case 2: dequant_k(ring[2 % PF_PDEPTH], tl); __syncthreads(); dequant_v(ring[2 % PF_PDEPTH], tl, IsTail{}); break;
+            default: dequant_k(ring[3 % PF_PDEPTH], tl); __syncthreads(); dequant_v(ring[3 % PF_PDEPTH], tl, IsTail{}); break;
             }
             __syncthreads();
         }
@@ -1223,9 +1286,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     // half-step a SIMD then holds one wave's QK MFMAs and the other's
     // exponentials and PV MFMAs.
     float16v_t sacc[PF_NST];  // S' of the tile between its two half-steps
-    // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile (stage kt & 1)
-    auto qk = [&](auto odd) __attribute__((always_inline)) {
-        const uint8_t *kst = decltype(odd)::value ? ldsk1 : ldsk0;
+    // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile (stage kst)
+    auto qk = [&](const uint8_t *kst) __attribute__((always_inline)) {
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
             {   // -m in all 16 accumulator registers, built as a 64-bit splat
@@ -1244,9 +1306,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
             }
         }
     };
-    // softmax and O += P V^ over tile kt (stage kt & 1)
-    auto sv = [&](int kt, auto odd) __attribute__((always_inline)) {
-        const uint8_t *vst = decltype(odd)::value ? ldsv1 : ldsv0;
+    // softmax and O += P V^ over tile kt (stage vst)
+    auto sv = [&](int kt, const uint8_t *vst) __attribute__((always_inline)) {
         const int kbase_t = PF_TK * (kt + ktb);
         if constexpr (MASK) {  // S' += mask[s][j][key] (natural log units -> log2)
             const uint16_t *mrow = p.mask + (int64_t)s * p.mask_bs + (int64_t)j * p.mask_rs;
@@ -1321,24 +1382,11 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     __syncthreads();  // the producers' first tile
     const bool grp_b = w >= PF_CWAVES / 2;  // uniform over the wave
     if (grp_b) __syncthreads();  // half-step 0
-    {
-        int kt = 0;
-        for (; kt + 2 <= ntk; kt += 2) {
-            qk(Even{});
-            __syncthreads();
-            sv(kt, Even{});
-            __syncthreads();
-            qk(Odd{});
-            __syncthreads();
-            sv(kt + 1, Odd{});
-            __syncthreads();
-        }
-        if (kt < ntk) {
-            qk(Even{});
-            __syncthreads();
-            sv(kt, Even{});
-            __syncthreads();
-        }
+    for (int kt = 0, stg = 0; kt < ntk; ++kt, stg = stg == PF_NSTAGE - 1 ? 0 : stg + 1) {
+        qk(ldsk + stg * PF_KBYTES);
+        __syncthreads();
+        sv(kt, ldsv + stg * PF_VBYTES);
+        __syncthreads();
     }
     if (!grp_b) __syncthreads();  // half-step 2 ntk (group B's last softmax)
 
@@ -1475,6 +1523,12 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     __shared__ int s_nsplit, s_nslot;
     const int B = p.num_seqs, tid = threadIdx.x;
     int carry = 0;
+    // image tiles of a prefill sequence: the key tiles of its last row tile
+    // (the longest causal range); a sequence past 2^20 of them (64M keys)
+    // leaves the whole call without images
+    constexpr int IMG_SEQ_MAX = 1 << 20;
+    long long icarry = 0;
+    int ibig = 0;
     for (int base = 0; base < B; base += PL_THREADS) {
         const int sq = base + tid;
         const int v = sq < B ? pl_tiles(p, sq) : 0;
@@ -1482,11 +1536,20 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         const int ex = pl_block_scan(v, s_tmp, &tot);
         if (sq < B) s_pre[sq] = carry + ex;
         carry += tot;
+        int vt = v > 0 ? pl_ntk(p, sq, v - 1) : 0;
+        ibig |= vt > IMG_SEQ_MAX;
+        vt = min(vt, IMG_SEQ_MAX);
+        int itot;
+        const int iex = pl_block_scan(vt, s_tmp, &itot);
+        if (p.pf_tbase != nullptr && sq < B) p.pf_tbase[sq] = (int)min(icarry + iex, (long long)INT32_MAX);
+        icarry += itot;
     }
+    const bool img_big = pl_block_max(ibig, s_red) != 0;
     if (tid == 0) {
         s_pre[B] = carry;
         s_nsplit = 0;
         s_nslot = 0;
+        if (p.pf_tbase != nullptr) p.pf_tbase[B] = (int)min(icarry, (long long)INT32_MAX);
     }
     for (int b = tid; b < PL_BUCKETS; b += PL_THREADS) s_bk[b] = 0;
     __syncthreads();
@@ -1631,6 +1694,73 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     if (tid == 0) {
         p.pf_count[0] = total;
         p.pf_count[1] = s_nsplit;
+        // the tile images: all of them in the workspace's image region, or
+        // none; and only where the row tiles read each tile PF_IMG_REUSE times
+        // on average (writing an image costs about what that many workgroups
+        // save by copying it instead of dequantizing)
+        const bool fit = p.pf_tiles != nullptr && !img_big && icarry <= INT32_MAX &&
+                         icarry <= p.pf_tiles_cap / ((long long)p.Hkv * PF_IMG_BYTES) &&
+                         W >= (long long)PF_IMG_REUSE * icarry;
+        p.pf_count[2] = fit ? 1 : 0;
+        p.pf_count[3] = fit ? (int)icarry : 0;
+    }
+}
+
+// Writes the dequantized tile images of a work-list launch (when the plan
+// kernel chose them): image (tbase[s] + kt) * Hkv + h holds K^ and V^T of
+// keys 64 kt .. 64 kt + 63 of sequence s, kv-head h, exactly as the prefill
+// producers would dequantize them into LDS (the same functions, so the same
+// bytes).  Sub-pages past the sequence's last key read its last valid
+// sub-page, and the V scales are made finite in every tile: keys past a row
+// tile's causal bound are masked to P = 0, which must meet finite V^.
+// Persistent grid; a workgroup's four waves dequantize the four sub-pages of
+// one image into LDS, then write it out in whole 16-byte rows per lane.
+template <bool VF16>
+__global__ __launch_bounds__(64 * PF_NSP) void prefill_tiles_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t img_lds[PF_IMG_BYTES];
+    if (p.pf_tiles == nullptr || p.pf_count[2] == 0) return;  // uniform
+    const int64_t n = (int64_t)p.pf_count[3] * p.Hkv;
+    const int lane = threadIdx.x & 63;
+    const int wsp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int B = p.num_seqs, Hkv = p.Hkv, bs = p.block_size;
+    constexpr int VSUB = VF16 ? 4096 : SUBPAGE_BYTES;
+    for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
+        const int tix = (int)(i / Hkv), h = (int)(i - (int64_t)tix * Hkv);
+        // its sequence: the last s < B with tbase[s] <= tix (sequences with no
+        // images share their successor's base), a 64-way search per step
+        int lo = 0, hi = B;
+        while (hi - lo > 1) {
+            const int step = (hi - lo + 63) >> 6;
+            const int idx = lo + lane * step;
+            const bool le = idx < hi && p.pf_tbase[idx] <= tix;
+            const uint64_t bal = __ballot(le);  // a prefix of the lanes, lane 0 included
+            const int k = 63 - __builtin_clzll(bal);
+            lo += k * step;
+            hi = min(hi, lo + step);
+        }
+        const int s = __builtin_amdgcn_readfirstlane(lo);
+        const int kt = tix - p.pf_tbase[s];
+        const int nq = p.qsl[s + 1] - p.qsl[s];
+        const int sl = p.seq_lens[s];
+        const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
+        const int kv_lim = p.causal ? min(sl, max(qa + nq, 0)) : sl;
+        const int sp = min(PF_NSP * kt + wsp, max((kv_lim - 1) >> 4, 0));
+        const int64_t page = p.bt[(int64_t)s * p.bt_stride + (16 * sp) / bs];
+        const int64_t spi = ((16 * sp) % bs) >> 4;
+        const uint8_t *kb = p.kc + (int64_t)h * p.chs + page * p.cbs + spi * SUBPAGE_BYTES;
+        const uint8_t *vb = p.vc + (int64_t)h * p.vchs + page * p.vcbs + spi * VSUB;
+        PfRaw r0, r1;
+        pf_fetch<VF16>(r0, kb, vb, lane, 0);
+        pf_fetch<VF16>(r1, kb, vb, lane, 1);
+        __syncthreads();  // the previous image has been written out
+        pf_dequant_k(r0, img_lds, wsp, lane, 0, p.pf_kmul);
+        pf_dequant_k(r1, img_lds, wsp, lane, 1, p.pf_kmul);
+        pf_dequant_v<true, VF16>(r0, img_lds + PF_KBYTES, wsp, lane, 0);
+        pf_dequant_v<true, VF16>(r1, img_lds + PF_KBYTES, wsp, lane, 1);
+        __syncthreads();
+        uint8_t *img = p.pf_tiles + i * PF_IMG_BYTES;
+        for (int o = 16 * threadIdx.x; o < PF_IMG_BYTES; o += 16 * 64 * PF_NSP)
+            *reinterpret_cast<u32x4 *>(img + o) = *reinterpret_cast<const u32x4 *>(img_lds + o);
     }
 }
 
@@ -1740,8 +1870,18 @@ struct Plan {
     int pf_split_max;   // split row tiles, at most
     int pf_slots_max;   // partial slots per kv head
     int pf_grid_items;  // work-list capacity: the prefill grid over Hkv
-    size_t off_items, off_split, off_pml, off_po, bytes;
+    size_t off_items, off_split, off_pml, off_po, off_tbase;
+    size_t bytes;       // the regions a call needs; the tile images follow at `bytes`
+    size_t img_bytes;   // room the tile images of the call's shape can take (capped)
 };
+
+// Workspace room for the prefill tile images, at most (bytes).  A call whose
+// images do not fit the workspace it is given dequantizes in the prefill
+// workgroups instead.
+#ifndef GFA_PF_IMG_CAP_MB
+#define GFA_PF_IMG_CAP_MB 1024
+#endif
+constexpr size_t PF_IMG_CAP = (size_t)GFA_PF_IMG_CAP_MB << 20;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1789,8 +1929,9 @@ void plan_add_class(Plan &pl, int nrg, int lo, int hi) {
 // work list even where a call would keep the 2-D prefill grid (bound only).
 // allow_split: reserve the partial slots of row tiles split over the keys
 // (without them the plan kernel leaves every row tile whole).
+// max_seq_len < 0: unknown (the image room is then the cap).
 void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_heads, bool force_pf,
-                 bool allow_split) {
+                 bool allow_split, int64_t max_seq_len) {
     pl.dec_rows_max = pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0;
     // row tiles over all sequences <= sum ceil(n_q * G / 256) <= T*G/256 + B
     const int pf_seqs = min(num_seqs, PL_MAX_SEQS);
@@ -1824,11 +1965,24 @@ void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_h
     const size_t prow = (size_t)pl.pf_slots_max * num_kv_heads * PF_ROWS;
     pl.off_pml = pl.off_split + align256((size_t)4 * pl.pf_split_max * sizeof(int));
     pl.off_po = pl.off_pml + align256(prow * 2 * sizeof(float));
-    pl.bytes = max(pl.off_po + align256(prow * 128 * sizeof(float)), (size_t)256);
+    // the per-sequence first image tile, then (optional) the images: every
+    // prefill sequence (n_q * G above the largest decode bound) at
+    // max_seq_len keys
+    pl.off_tbase = pl.off_po + align256(prow * 128 * sizeof(float));
+    pl.bytes = max(pl.off_tbase + (pf ? align256((size_t)(num_seqs + 1) * sizeof(int)) : 0), (size_t)256);
+    pl.img_bytes = 0;
+    if (pf) {
+        const int64_t nq_min = pl.dec_rows_max / max(G, 1) + 1;  // a prefill sequence's query tokens, at least
+        const int64_t npf = max((int64_t)1, min((int64_t)num_seqs, max(num_tokens, (int64_t)0) / nq_min));
+        const double want = max_seq_len < 0 ? (double)PF_IMG_CAP
+                                            : (double)npf * (double)((max_seq_len + PF_TK - 1) / PF_TK) *
+                                                  num_kv_heads * PF_IMG_BYTES;
+        pl.img_bytes = want >= (double)PF_IMG_CAP ? PF_IMG_CAP : align256((size_t)want);
+    }
 }
 
 Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int max_query_len,
-               bool allow_split = true) {
+               int64_t max_seq_len, bool allow_split = true) {
     Plan pl;
     const int G = num_heads / num_kv_heads;
     const int max_rows = max_query_len * G;
@@ -1845,7 +1999,7 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
         if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, hi2);
     }
     pl.need_prefill = max_rows > (pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0);
-    plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split);
+    plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split, max_seq_len);
     return pl;
 }
 
@@ -1863,7 +2017,7 @@ Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num
     if (G <= 16) plan_add_class(pl, 1, 0, 16);
     if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, DEC_CHUNK_ROWS);
     pl.need_prefill = true;
-    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split);
+    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, -1);
     return pl;
 }
 
@@ -1896,6 +2050,10 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
         }
     }
     if (pl.need_prefill) {
+        // the tile images, after the decode launches (their write-back then
+        // overlaps the MFMA-bound prefill, not the HBM-bound decode); returns
+        // at once when the plan chose none
+        if (p.pf_seq && p.pf_tiles) prefill_tiles_kernel<false><<<device_cus() * 4, 64 * PF_NSP, 0, stream>>>(p);
         const int rows = max_query_len * p.G;
         const int tiles = (rows + PF_ROWS - 1) / PF_ROWS;
         const dim3 grid = p.pf_seq ? dim3(pl.pf_grid_items * num_kv_heads) : dim3(tiles * num_kv_heads, num_seqs);
@@ -1913,9 +2071,9 @@ extern "C" size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int
                                                                int head_size, int max_query_len,
                                                                int max_seq_len) {
     (void)head_size;
-    (void)max_seq_len;
     if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads) return 0;
-    return make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1)).bytes;
+    const Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1), max(max_seq_len, 1));
+    return pl.bytes + pl.img_bytes;
 }
 
 extern "C" size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs, int64_t max_num_tokens,
@@ -1925,7 +2083,8 @@ extern "C" size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs
     if (max_num_seqs <= 0 || max_num_tokens < 0 || num_kv_heads <= 0 || num_heads <= 0 ||
         num_heads % num_kv_heads)
         return 0;
-    return bound_plan(max_num_seqs, max_num_tokens, num_heads, num_kv_heads, true).bytes;
+    const Plan pl = bound_plan(max_num_seqs, max_num_tokens, num_heads, num_kv_heads, true);
+    return pl.bytes + pl.img_bytes;
 }
 
 extern "C" int gfx906_fa_amd_device_cus(void) { return device_cus(); }
@@ -1934,13 +2093,13 @@ extern "C" int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tok
                                                        int num_kv_heads, int head_size, int max_query_len,
                                                        int max_seq_len, int64_t *info, int info_len) {
     (void)head_size;
-    (void)max_seq_len;
     if (info == nullptr || num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads)
         return -1;
-    const Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1));
-    const int64_t v[] = {(int64_t)pl.bytes, pl.ndc, pl.dec_rows_max, pl.need_prefill ? 1 : 0,
+    const Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1), max(max_seq_len, 1));
+    const int64_t v[] = {(int64_t)(pl.bytes + pl.img_bytes), pl.ndc, pl.dec_rows_max, pl.need_prefill ? 1 : 0,
                          pl.pf_items_max, pl.pf_grid_items, pl.pf_split_max, pl.pf_slots_max,
-                         pl.pf_items_max ? (int64_t)pl.off_items : -1, device_cus()};
+                         pl.pf_items_max ? (int64_t)pl.off_items : -1, device_cus(), (int64_t)pl.bytes,
+                         (int64_t)pl.img_bytes};
     const int n = (int)(sizeof(v) / sizeof(v[0]));
     for (int i = 0; i < n && i < info_len; ++i) info[i] = v[i];
     return n;
@@ -2034,12 +2193,13 @@ hipError_t paged_attention_impl(
         return hipErrorInvalidValue;
     }
     const int G = num_heads / num_kv_heads;
-    Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1));
+    Plan pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1), max(max_seq_len, 1));
     if (noalloc) {
         // the library's scratch array instead of a caller workspace; a plan
         // whose split-prefill partials do not fit leaves row tiles unsplit
         if (pl.bytes > GFX906_FA_AMD_SCRATCH_BYTES)
-            pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1), false);
+            pl = make_plan(num_seqs, num_tokens, num_heads, num_kv_heads, max(max_query_len, 1),
+                           max(max_seq_len, 1), false);
         if (pl.bytes > GFX906_FA_AMD_SCRATCH_BYTES) {
             fprintf(stderr,
                     "[gfx906_fa_amd] paged_attention_noalloc: this batch needs %zu bytes of scratch, more than "
@@ -2097,6 +2257,12 @@ hipError_t paged_attention_impl(
     p.pf_split = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_split) : nullptr;
     p.pf_ml = pl.pf_items_max ? reinterpret_cast<float *>(ws + pl.off_pml) : nullptr;
     p.pf_o = pl.pf_items_max ? reinterpret_cast<float *>(ws + pl.off_po) : nullptr;
+    // tile images: whatever room the workspace has past the call's regions
+    p.pf_tbase = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_tbase) : nullptr;
+    const size_t img_room = workspace_bytes > pl.bytes ? workspace_bytes - pl.bytes : 0;
+    p.pf_tiles = (pl.pf_items_max && img_room >= (size_t)PF_IMG_BYTES) ? reinterpret_cast<uint8_t *>(ws + pl.bytes)
+                                                                       : nullptr;
+    p.pf_tiles_cap = p.pf_tiles ? (int64_t)img_room : 0;
     // decode workspace pointers are set per decode class in launch_all
     p.ws_hdr = nullptr;
     p.ws_pre = nullptr;

@@ -386,14 +386,20 @@ def workspace_bound(max_num_seqs: int, max_num_tokens: int, num_heads: int, num_
 
 
 PLAN_FIELDS = ("bytes", "decode_classes", "dec_rows_max", "prefill", "pf_items_max", "pf_grid_items",
-               "pf_split_max", "pf_slots_max", "pf_header_offset", "cus")
+               "pf_split_max", "pf_slots_max", "pf_header_offset", "cus", "img_offset", "img_bytes")
 
 
 def plan_info(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int, max_query_len: int,
               max_seq_len: int, head_size: int = 128) -> dict:
     """The launch plan of a call shape (see PLAN_FIELDS).  ``pf_header_offset``
     is where, in the workspace, the call leaves its prefill work-list header:
-    int32 item count, int32 count of row tiles split over the keys."""
+    int32 item count, int32 count of row tiles split over the keys, int32 1
+    when the prefill tiles were dequantized once into the workspace as LDS
+    images (else 0), int32 their count per kv head.  ``bytes`` (the
+    workspace_size) is ``img_offset``, the regions every call needs, plus
+    ``img_bytes`` of room for those images; a smaller workspace of at least
+    ``img_offset`` bytes runs the same call with the prefill workgroups
+    dequantizing every tile themselves."""
     buf = (ctypes.c_int64 * len(PLAN_FIELDS))()
     n = _load().gfx906_fa_amd_paged_attention_plan_info(num_seqs, num_tokens, num_heads, num_kv_heads,
                                                          head_size, max_query_len, max_seq_len, buf,
@@ -451,8 +457,14 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
     _check(out.dtype in _DT and out.dim() == 3 and tuple(out.shape[1:]) == (Hq, D)
            and out.shape[0] >= T and out.stride(2) == 1, "out must be [num_tokens, Hq, 128] fp32/fp16/bf16")
     need = workspace_size(B, T, Hq, Hkv, max_query_len, max_seq_len)
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
+    if workspace is None:
         workspace = new_workspace(need, query.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        # the prefill tile-image room is optional: a workspace with the regions
+        # every call needs runs as given (its prefill workgroups dequantize)
+        have = workspace.numel() * workspace.element_size()
+        if have < plan_info(B, T, Hq, Hkv, max_query_len, max_seq_len, D)["img_offset"]:
+            workspace = new_workspace(need, query.device)
     _check(workspace.data_ptr() % 256 == 0, "workspace must be 256-byte aligned")
     ws_bytes = workspace.numel() * workspace.element_size()
     if new_key is not None or new_value is not None or slot_mapping is not None:

@@ -200,6 +200,13 @@ hipError_t gfx906_fa_amd_rope_cache_write_kv(
  *     contiguous share of all their 16-token KV sub-pages; segments cut
  *     between workgroups leave partial (m, l, O) in the workspace and a
  *     second kernel merges them.
+ *     A prefill call also takes room for its 64-key tiles dequantized once
+ *     to fp16 (35840 bytes per tile and kv-head, every prefill sequence at
+ *     max_seq_len keys, at most 1 GiB): the tiles are then written once and
+ *     copied into LDS by every workgroup that reads them.  Any workspace of
+ *     at least plan_info()'s img_offset bytes runs the same call; when the
+ *     images do not fit the room it has, the prefill workgroups dequantize
+ *     each tile themselves (same outputs, bit for bit).
  */
 size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int num_tokens,
                                                     int num_heads, int num_kv_heads,
@@ -210,7 +217,8 @@ size_t gfx906_fa_amd_paged_attention_workspace_size(int num_seqs, int num_tokens
  *     current device with num_seqs <= max_num_seqs and num_tokens <=
  *     max_num_tokens, whatever max_query_len and the mix of decode,
  *     speculative-verify and prefill sequences: what a serving loop reserves
- *     once, before graph capture, for a layer's (num_heads, num_kv_heads).
+ *     once, before graph capture, for a layer's (num_heads, num_kv_heads)
+ *     (the prefill tile-image room at its 1 GiB cap included).
  *     No reference counterpart (the reference grows its buffers per call,
  *     extension/gfx906_fa_backend.py:316-403). */
 size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs, int64_t max_num_tokens,
@@ -223,8 +231,11 @@ size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs, int64_t m
  *     [5] prefill work-list capacity, [6] split row tiles (bound), [7]
  *     partial slots per kv-head, [8] byte offset in the workspace of the
  *     prefill work-list header (int32 item count, int32 split row tile count,
- *     written by the call; -1 without a work list), [9] CUs planned for.
- *     Returns the number of entries (10; at most info_len are written), or
+ *     int32 1 if the tiles were dequantized once as images, int32 image
+ *     tiles per kv-head; written by the call; -1 without a work list), [9]
+ *     CUs planned for, [10] the workspace bytes every call needs (the image
+ *     room starts there), [11] the image room (info[0] = [10] + [11]).
+ *     Returns the number of entries (12; at most info_len are written), or
  *     -1 for an invalid shape.  No reference counterpart. */
 int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tokens, int num_heads,
                                             int num_kv_heads, int head_size, int max_query_len,
