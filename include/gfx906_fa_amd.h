@@ -264,7 +264,10 @@ hipError_t gfx906_fa_amd_paged_attention(
  *      process ends.  Decode / verify plans are those of (5), so outputs
  *      are bit-identical to (5); a batch whose split-prefill partials would
  *      not fit in the scratch runs its prefill row tiles unsplit (same
- *      tolerance, different summation order).  A batch whose plan still
+ *      tolerance, different summation order); prefill tile images are
+ *      written only when they fit the scratch past the plan (otherwise the
+ *      prefill workgroups dequantize their own tiles, same bytes).  A batch
+ *      whose plan still
  *      exceeds the scratch is rejected (hipErrorInvalidValue and a line on
  *      stderr) before any work is enqueued.  Every call on a device shares
  *      that device's scratch: calls that overlap on one device (concurrent
