@@ -2257,11 +2257,17 @@ hipError_t paged_attention_impl(
     p.pf_split = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_split) : nullptr;
     p.pf_ml = pl.pf_items_max ? reinterpret_cast<float *>(ws + pl.off_pml) : nullptr;
     p.pf_o = pl.pf_items_max ? reinterpret_cast<float *>(ws + pl.off_po) : nullptr;
-    // tile images: whatever room the workspace has past the call's regions
+    // tile images: whatever room the workspace has past the call's regions.
+    // None when no sequence can have PF_IMG_REUSE row tiles: the row tiles
+    // then read each key tile fewer times than that on average (a sequence's
+    // row tiles each read at most the key tiles of its last), so the plan
+    // would decline them, and the pre-pass launch is skipped.
     p.pf_tbase = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_tbase) : nullptr;
     const size_t img_room = workspace_bytes > pl.bytes ? workspace_bytes - pl.bytes : 0;
-    p.pf_tiles = (pl.pf_items_max && img_room >= (size_t)PF_IMG_BYTES) ? reinterpret_cast<uint8_t *>(ws + pl.bytes)
-                                                                       : nullptr;
+    const bool img_reuse = ((int64_t)max_query_len * G + PF_ROWS - 1) / PF_ROWS >= PF_IMG_REUSE;
+    p.pf_tiles = (pl.pf_items_max && img_reuse && img_room >= (size_t)PF_IMG_BYTES)
+                     ? reinterpret_cast<uint8_t *>(ws + pl.bytes)
+                     : nullptr;
     p.pf_tiles_cap = p.pf_tiles ? (int64_t)img_room : 0;
     // decode workspace pointers are set per decode class in launch_all
     p.ws_hdr = nullptr;
