@@ -396,6 +396,159 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
     }
 }
 
+// One 16-byte-per-lane copy from global memory straight into LDS
+// (global_load_lds_dwordx4: lane i writes lds + 16 i), issued from inline
+// assembly.  The compiler counts an LDS DMA issued through its builtin as
+// both a global and an LDS access: while one is in flight it waits for every
+// LDS read at once (lgkmcnt(0)) and drains the copies at barriers, which
+// takes away the overlap the copies are for.  Issued here, the copies are
+// invisible to it, and the caller waits for them itself (vmcnt; loads
+// complete in order, so any later vector-memory instruction only makes such
+// a wait stricter).  M0 holds the LDS address; its previous value is put
+// back.  NT: the nontemporal hint (bytes read once; as the register path's
+// K/V loads).
+template <bool NT>
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
+    uint32_t saved;
+    if constexpr (NT)
+        asm volatile("s_mov_b32 %0, m0\n\t"
+                     "s_mov_b32 m0, %2\n\t"
+                     "global_load_lds_dwordx4 %1, off nt\n\t"
+                     "s_mov_b32 m0, %0"
+                     : "=&s"(saved)
+                     : "v"(src), "s"(lds)
+                     : "memory");
+    else
+        asm volatile("s_mov_b32 %0, m0\n\t"
+                     "s_mov_b32 m0, %2\n\t"
+                     "global_load_lds_dwordx4 %1, off\n\t"
+                     "s_mov_b32 m0, %0"
+                     : "=&s"(saved)
+                     : "v"(src), "s"(lds)
+                     : "memory");
+}
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int DEC_RING_SLOT = 2 * SUBPAGE_BYTES;     // K then V sub-page
+#ifndef GFA_DEC_RING
+#define GFA_DEC_RING 3
+#endif
+constexpr int DEC_RING = GFA_DEC_RING;               // LDS ring slots per wave (verify tiles)
+constexpr int DEC_RING_DMA = 6;                      // copies per sub-page and wave
+static_assert(SUBPAGE_BYTES == 2 * 1024 + 128, "two full copies and an 8-lane one per sub-page");
+
+// stream_range with the sub-pages staged through a per-wave LDS ring of
+// DEPTH slots (ring: this wave's LDS, DEPTH * DEC_RING_SLOT bytes): sub-page
+// j + DEPTH - 1 is copied into slot (j + DEPTH - 1) % DEPTH while sub-page j
+// is computed, so DEPTH - 1 sub-pages are in flight per wave with no
+// registers held for them.  The slot a copy fills was read into registers
+// (and consumed) in the previous step.
+template <int NRG, int DEPTH>
+__device__ __forceinline__ void stream_range_lds(WaveAcc<NRG> &acc, const AttnParams &p, int s, int h,
+                                                 int wb, int we, const half8_t (&qf)[NRG][4],
+                                                 const int (&lim)[NRG], int lane, int i16, int g, int j0,
+                                                 int jstep, uint8_t *ring) {
+    const int nall = (we - wb + 15) >> 4;
+    const int nsub = nall > j0 ? (nall - j0 + jstep - 1) / jstep : 0;  // this wave's sub-pages
+    if (nsub <= 0) return;
+    const int32_t *btrow = p.bt + (int64_t)s * p.bt_stride;
+    const uint8_t *kbase = p.kc + (int64_t)h * p.chs;
+    const uint8_t *vbase = p.vc + (int64_t)h * p.chs;
+    const int spp = p.block_size >> 4;  // sub-pages per page
+    auto load_pg = [&](int chunk, int &spi) -> int {
+        const int j = 64 * chunk + lane;
+        const int sp = (wb >> 4) + j0 + jstep * j;  // the sub-page's index in the sequence
+        const int pi = sp / spp;
+        spi = sp - pi * spp;
+        return j < nsub ? btrow[pi] : 0;
+    };
+    // A window load is waited for where it is issued (once per 64
+    // sub-pages): the compiler does not see the ring's copies, so a window
+    // register still pending at its v_readlane would take a vmcnt(0) there,
+    // draining every copy in flight.
+    auto ready = [](int &v) __attribute__((always_inline)) { asm volatile("" : "+v"(v)); };
+    int ps_cur = 0, ps_nxt = 0;
+    int pg_cur = load_pg(0, ps_cur);
+    int pg_nxt = nsub > 64 ? load_pg(1, ps_nxt) : 0;
+    ready(pg_cur);
+    ready(pg_nxt);
+    int chunk = 0;
+    int lim_min = lim[0];
+#pragma unroll
+    for (int rg = 1; rg < NRG; ++rg) lim_min = min(lim_min, lim[rg]);
+    {
+        const float f = (float)min(lim_min, 1 << 24);
+        lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
+    }
+    const float c = p.scale_log2e;
+    const LaneOffsets lo = lane_offsets(i16, g);
+    const uint32_t ring_lds =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring);
+
+    // copies of sub-page j into slot sl: exactly DEC_RING_DMA per wave
+    auto fetch = [&](int j, int sl) __attribute__((always_inline)) {
+        if (j < nsub) {  // uniform
+            if ((j >> 6) != chunk) {  // advance the page-id window (uniform)
+                chunk = j >> 6;
+                pg_cur = pg_nxt;
+                ps_cur = ps_nxt;
+                pg_nxt = 64 * (chunk + 1) < nsub ? load_pg(chunk + 1, ps_nxt) : 0;
+                ready(pg_nxt);
+            }
+            const int64_t page = __builtin_amdgcn_readlane(pg_cur, j & 63);
+            const int spi = __builtin_amdgcn_readlane(ps_cur, j & 63);
+            const int64_t off = page * p.cbs + (int64_t)spi * SUBPAGE_BYTES;
+            const uint8_t *kb = kbase + off + 16 * lane, *vb = vbase + off + 16 * lane;
+            const uint32_t dk = ring_lds + sl * DEC_RING_SLOT, dv = dk + SUBPAGE_BYTES;
+            constexpr bool NT = GFA_DEC_NT != 0;
+            lds_dma16<NT>(kb, dk);
+            lds_dma16<NT>(kb + 1024, dk + 1024);
+            lds_dma16<NT>(vb, dv);
+            lds_dma16<NT>(vb + 1024, dv + 1024);
+            if (lane < 8) {  // the last 128 bytes of each
+                lds_dma16<NT>(kb + 2048, dk + 2048);
+                lds_dma16<NT>(vb + 2048, dv + 2048);
+            }
+        }
+    };
+    // sub-page j has landed: the copies of the DEPTH - 1 later sub-pages may
+    // still be in flight (all of them issued), else wait for every copy
+    auto landed = [&](int j) __attribute__((always_inline)) {
+        static_assert(DEC_RING_DMA * (DEPTH - 1) <= 63, "vmcnt immediate");
+        if (j + DEPTH - 1 < nsub) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DEC_RING_DMA * (DEPTH - 1)) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+#pragma unroll
+    for (int u = 0; u < DEPTH - 1; ++u) fetch(u, u);
+    for (int base = 0; base < nsub; base += DEPTH) {
+#pragma unroll
+        for (int u = 0; u < DEPTH; ++u) {
+            const int j = base + u;
+            if (j < nsub) {  // uniform
+                // the previous step's reads of the slot refilled next have
+                // completed (their values were consumed, but the compiler may
+                // place the last uses after this point)
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                fetch(j + DEPTH - 1, (u + DEPTH - 1) % DEPTH);
+                landed(j);
+                const uint8_t *sb = ring + u * DEC_RING_SLOT;
+                SubPage sp;
+                sp.kq[0] = *reinterpret_cast<const u32x4 *>(sb + lo.kq);
+                sp.kq[1] = *reinterpret_cast<const u32x4 *>(sb + lo.kq + 1024);
+                sp.ks = *reinterpret_cast<const u32x2 *>(sb + lo.ks);
+                sp.vq[0] = *reinterpret_cast<const u32x4 *>(sb + SUBPAGE_BYTES + lo.vq);
+                sp.vq[1] = *reinterpret_cast<const u32x4 *>(sb + SUBPAGE_BYTES + lo.vq + 1024);
+                sp.vs[0] = *reinterpret_cast<const u32x4 *>(sb + SUBPAGE_BYTES + lo.vs);
+                sp.vs[1] = *reinterpret_cast<const u32x4 *>(sb + SUBPAGE_BYTES + lo.vs + 16);
+                const int tok0 = wb + 16 * (j0 + jstep * j);
+                attend_subpage<NRG>(acc, sp, qf, tok0, we, lim, c, g,
+                                    !(tok0 + 16 <= we && tok0 + 15 <= lim_min));
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (every copy was waited for above)
+}
+
 // ---------------------------------------------------------------------------
 // Decode / speculative-verify kernel (stream-K over workgroups).
 //
@@ -642,7 +795,10 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
 
-    __shared__ float sm_o[DEC_NW][R][128 + 4];
+    // per wave: its merge rows, or (verify tiles) its LDS ring while it
+    // streams; rows past R only lengthen the slice for the ring
+    constexpr int RA = NRG == 2 ? cmax(R, (DEC_RING * DEC_RING_SLOT + 4 * 132 - 1) / (4 * 132)) : R;
+    __shared__ float sm_o[DEC_NW][RA][128 + 4];
     __shared__ float sm_m[DEC_NW][R], sm_l[DEC_NW][R];
     int64_t u = u0;
     bool first = true;
@@ -668,9 +824,15 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         load_rows<NRG, QDT>(p, h, si.q0, nrows, rc, si.sl, si.qa, i16, g, qf, lim);
         WaveAcc<NRG> acc;
         acc_init(acc);
-        stream_range<NRG, GFA_DEC_NT != 0, DecCfg<NRG>::depth>(acc, p, s, h, 16 * a,
-                                                                 min(16 * b, si.kv_lim), qf, lim,
-                                                                 lane, i16, g, j0, jstep);
+        if constexpr (NRG == 2) {  // verify tiles: sub-pages staged through this wave's sm_o slice
+            static_assert(sizeof(sm_o[0]) >= DEC_RING * DEC_RING_SLOT, "ring fits the wave's slice");
+            stream_range_lds<NRG, DEC_RING>(acc, p, s, h, 16 * a, min(16 * b, si.kv_lim), qf, lim, lane, i16,
+                                            g, j0, jstep, reinterpret_cast<uint8_t *>(&sm_o[wv][0][0]));
+        } else {
+            stream_range<NRG, GFA_DEC_NT != 0, DecCfg<NRG>::depth>(acc, p, s, h, 16 * a,
+                                                                     min(16 * b, si.kv_lim), qf, lim,
+                                                                     lane, i16, g, j0, jstep);
+        }
         // ---- merge the chunk's waves' states in LDS ------------------------
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
