@@ -1005,13 +1005,17 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 //     kernel and the running row max m fed in as the accumulator input;
 //   producers (waves 8-11, one per SIMD): wave 8 + i fetches sub-page i of
 //     every tile from HBM, PF_PDEPTH tiles ahead, and dequantizes it into
-//     the LDS stage the consumers read next.
+//     the LDS stage the consumers read next - or, when the plan wrote the
+//     launch's tile images (each tile dequantized once into the workspace by
+//     prefill_tiles_kernel), copies a quarter of each image straight into
+//     LDS (global_load_lds).
 // A consumer's only LDS traffic is its MFMA operand reads, so the waits in
 // front of its MFMAs never queue behind dequant stores (LDS instructions of
 // one wave complete in order), and the dequant VALU work issues from a wave
-// of its own beside the two consumers' MFMAs.  The roles share one barrier
-// per tile: iteration kt, the consumers attend over tile kt (stage kt&1)
-// while the producers fill stage (kt+1)&1 with tile kt+1.
+// of its own beside the two consumers' MFMAs.  Tile t sits in LDS stage
+// t % 3.  The two consumer waves of a SIMD run half a tile apart (two
+// barriers per tile, the half-steps below); the producers write K^ of tile
+// t in half-step 2t - 2 and V^T in 2t - 1.
 // 32x32x16 operand layout (lane l, h = l/32): A[i = l%32][k = 8h+e],
 // B[k = 8h+e][j = l%32], D[i = 8(r/4)+4h+r%4][j = l%32] for register r.  A
 // lane's S^T registers 8s..8s+7 are then exactly the keys its P^T operand
