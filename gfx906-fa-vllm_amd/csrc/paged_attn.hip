@@ -2097,7 +2097,7 @@ void plan_add_class(Plan &pl, int nrg, int lo, int hi) {
 // (without them the plan kernel leaves every row tile whole).
 // max_seq_len < 0: unknown (the image room is then the cap).
 void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_heads, bool force_pf,
-                 bool allow_split, int64_t max_seq_len) {
+                 bool allow_split, int64_t max_seq_len, int64_t max_query_len) {
     pl.dec_rows_max = pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0;
     // row tiles over all sequences <= sum ceil(n_q * G / 256) <= T*G/256 + B
     const int pf_seqs = min(num_seqs, PL_MAX_SEQS);
@@ -2136,8 +2136,10 @@ void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_h
     // max_seq_len keys
     pl.off_tbase = pl.off_po + align256(prow * 128 * sizeof(float));
     pl.bytes = max(pl.off_tbase + (pf ? align256((size_t)(num_seqs + 1) * sizeof(int)) : 0), (size_t)256);
+    // (no image room where no sequence can have PF_IMG_REUSE row tiles: the
+    // launch then never writes images, see the call's image pointer)
     pl.img_bytes = 0;
-    if (pf) {
+    if (pf && (max(max_query_len, (int64_t)0) * G + PF_ROWS - 1) / PF_ROWS >= PF_IMG_REUSE) {
         const int64_t nq_min = pl.dec_rows_max / max(G, 1) + 1;  // a prefill sequence's query tokens, at least
         const int64_t npf = max((int64_t)1, min((int64_t)num_seqs, max(num_tokens, (int64_t)0) / nq_min));
         const double want = max_seq_len < 0 ? (double)PF_IMG_CAP
@@ -2165,7 +2167,7 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
         if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, hi2);
     }
     pl.need_prefill = max_rows > (pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0);
-    plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split, max_seq_len);
+    plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split, max_seq_len, max_query_len);
     return pl;
 }
 
@@ -2183,7 +2185,7 @@ Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num
     if (G <= 16) plan_add_class(pl, 1, 0, 16);
     if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, DEC_CHUNK_ROWS);
     pl.need_prefill = true;
-    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, -1);
+    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, -1, max_num_tokens);
     return pl;
 }
 

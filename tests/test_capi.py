@@ -103,18 +103,26 @@ def test_workspace_size_plan():
     assert cus > 0
     pf = gfx906_fa.workspace_size(1, 50, 48, 8, 50, 65586)
     assert pf >= 3 * (-(-cus // 8)) * 8 * 256 * 130 * 4
-    # ... plus room for its 64-key tiles dequantized once (35840 bytes per
-    # tile and kv head, one prefill sequence here), capped at 1 GiB; the
-    # regions every call needs do not depend on the context length
-    i1 = gfx906_fa.plan_info(1, 50, 48, 8, 50, 65586)
-    i2 = gfx906_fa.plan_info(1, 50, 48, 8, 50, 1 << 20)
+    # A launch whose sequences can have 32 row tiles (2048 tokens x 6 q-heads
+    # = 48 here) also takes room for its 64-key tiles dequantized once
+    # (35840 bytes per tile and kv head, one prefill sequence here), capped
+    # at 1 GiB; the regions every call needs do not depend on the context
+    # length
+    i1 = gfx906_fa.plan_info(1, 2048, 48, 8, 2048, 65586)
+    i2 = gfx906_fa.plan_info(1, 2048, 48, 8, 2048, 1 << 20)
     assert i1["img_offset"] == i2["img_offset"] and i1["img_offset"] % 256 == 0
     assert i1["img_bytes"] == -(-(65586 // 64 + 1) * 8 * 35840 // 256) * 256
     assert i2["img_bytes"] == 1 << 30
-    assert pf == i1["img_offset"] + i1["img_bytes"]
-    assert gfx906_fa.workspace_size(1, 50, 48, 8, 50, 1 << 20) == i2["img_offset"] + (1 << 30)
-    # a decode-only shape takes no image room
+    assert gfx906_fa.workspace_size(1, 2048, 48, 8, 2048, 65586) == i1["img_offset"] + i1["img_bytes"]
+    assert gfx906_fa.workspace_size(1, 2048, 48, 8, 2048, 1 << 20) == i2["img_offset"] + (1 << 30)
+    # the 50-token chunk (2 row tiles) and a decode-only shape take none
+    assert gfx906_fa.plan_info(1, 50, 48, 8, 50, 65586)["img_bytes"] == 0
+    assert pf == gfx906_fa.plan_info(1, 50, 48, 8, 50, 65586)["img_offset"]
     assert gfx906_fa.plan_info(32, 32, 48, 8, 1, 16384)["img_bytes"] == 0
+    # the bar: 32 row tiles (8192 rows at one q-head per kv-head) take room,
+    # 31 (7936 rows) none
+    assert gfx906_fa.plan_info(1, 8192, 8, 8, 8192, 9000)["img_bytes"] > 0
+    assert gfx906_fa.plan_info(1, 7936, 8, 8, 7936, 9000)["img_bytes"] == 0
     # kv-head counts that do not divide the CU count round the slots up per head
     for hkv in (3, 5, 7, 12):
         need = 3 * (-(-cus // hkv)) * hkv * 256 * 130 * 4

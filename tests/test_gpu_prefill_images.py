@@ -9,7 +9,9 @@ Shapes: a long prompt, a prompt with one query head per kv head whose row
 tiles are split over the keys (pieces start past key tile 0), block size 64,
 a mixed batch with decode sequences, explicit query positions without the
 causal mask; and a short chunk on a long prefix, read about twice per tile,
-which keeps the in-kernel dequantization although the room is there
+which gets no image room (no sequence has 32 row tiles), and a 40-row-tile
+prompt, which gets the room but whose row tiles read each key tile about
+20 times on average, so the plan keeps the in-kernel dequantization
 (reference: tests/test_inline_causal.py, tests/test_fa_mixed_batch.py)."""
 import numpy as np
 import pytest
@@ -28,6 +30,7 @@ CASES = [
     ("bs64 G=1", [20000, 3000], [20000, 3000], 4, 4, 64, "f16", True),
     ("mixed with decodes", [4000, 70, 5000, 333, 1200], [400, 1, 5000, 5, 1], 32, 4, 32, "bf16", True),
     ("chunk on a long prefix", [20000 + 60], [60], 48, 8, 16, "f16", False),
+    ("prompt below the reuse bar", [10240], [10240], 1, 1, 16, "f16", False),
 ]
 
 
@@ -47,7 +50,8 @@ def _run(b, nbytes, q_abs=None, causal=True):
 
 def _both(b, q_abs=None, causal=True, images=True):
     info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
-    assert info["prefill"] == 1 and info["pf_header_offset"] >= 0 and info["img_bytes"] > 0
+    assert info["prefill"] == 1 and info["pf_header_offset"] >= 0
+    assert (info["img_bytes"] > 0) == (b.max_query_len * b.Hq // b.Hkv > 31 * 256), info
     out_i, ws_i = _run(b, info["bytes"], q_abs, causal)
     out_d, ws_d = _run(b, info["img_offset"], q_abs, causal)
     hi, hd = _header(ws_i, info["pf_header_offset"]), _header(ws_d, info["pf_header_offset"])
