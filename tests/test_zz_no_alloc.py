@@ -82,6 +82,21 @@ def test_noalloc_prefill_and_mixed():
         assert_close(to_np_f32(out), batch_oracle(b))
 
 
+def test_noalloc_prompt_with_tile_images():
+    """A 3000-token prompt at 48/8: its row tiles read each key tile about 37
+    times, so the plan writes the 64-key tile images (13.5 MB, room the
+    scratch has past this unsplit plan); the output equals the workspace
+    entry's (which takes the same path) bit for bit."""
+    need_gpu()
+    announce("noalloc prompt 3000 48/8 with tile images")
+    b = W.build_batch([3000], [3000], 48, 8, dtype="bf16", seed=75)
+    ref = _with_workspace(b, torch.float32)
+    out = torch.full_like(ref, 3.0)
+    _noalloc(b, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
 def test_noalloc_rejects_oversize_batch():
     """A batch whose plan exceeds the scratch is refused before any work."""
     need_gpu()
