@@ -98,9 +98,11 @@ struct AttnParams {
     // fp16 K^ and V^T of 64-key tile kt of prefill sequence s for kv-head h,
     // byte for byte the prefill kernel's LDS stages, at image
     // (pf_tbase[s] + kt) * Hkv + h of pf_tiles, written once per call by
-    // prefill_tiles_kernel when every image fits pf_tiles_cap bytes (the plan
-    // kernel sets pf_count[2]); the prefill workgroups then copy them into
-    // LDS instead of dequantizing every tile themselves.
+    // prefill_tiles_kernel when every image fits pf_tiles_cap bytes and the
+    // row tiles read each key tile PF_IMG_REUSE times on average (the plan
+    // kernel decides: pf_count[2], pf_count[3] = image tiles per kv-head);
+    // the prefill workgroups then copy them into LDS instead of dequantizing
+    // every tile themselves.
     uint8_t *pf_tiles;
     int *pf_tbase;      // per sequence (num_seqs + 1): first image tile
     int64_t pf_tiles_cap;
