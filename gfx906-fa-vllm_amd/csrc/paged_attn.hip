@@ -993,6 +993,62 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
 }
 
+// The same merge for segments of few pieces (a batch whose resident
+// workgroups are few per segment): one workgroup per (sequence, kv-head),
+// thread t takes d-chunk t % 32 of rows t / 32, t / 32 + 8, ... and merges
+// the segment's pieces in order, the loads of up to 8 of them in flight.
+template <int ODT>
+__global__ __launch_bounds__(256) void attn_combine_few_kernel(AttnParams p) {
+    const int s = blockIdx.x, h = blockIdx.y;
+    const int64_t U = p.ws_hdr[0];
+    const int nwg = (int)p.ws_hdr[1];
+    const int pre = p.ws_pre[s];
+    const SegInfo si = seg_info(p, s);
+    if (si.nsub == 0 || U == 0) return;
+    const int64_t S0 = (int64_t)pre * p.Hkv + (int64_t)h * si.nsub;
+    const int wf = range_of(U, S0, nwg), wl = range_of(U, S0 + si.nsub - 1, nwg);
+    if (wf == wl && range_start(U, wf, nwg) <= S0 && range_start(U, wf + 1, nwg) >= S0 + si.nsub)
+        return;  // whole segment in one workgroup: already written
+    const int rows = si.nq * p.G;
+    const int dc = threadIdx.x & 31, d0 = 4 * dc;
+    constexpr int CU = 8;
+    for (int r = threadIdx.x >> 5; r < rows; r += 8) {
+        float m = -INFINITY, l = 0.f;
+        float4_t o = {0.f, 0.f, 0.f, 0.f};
+        for (int k0 = wf; k0 <= wl; k0 += CU) {
+            float2_t mlk[CU];
+            float4_t ok[CU];
+#pragma unroll
+            for (int i = 0; i < CU; ++i) {
+                const int k = k0 + i;
+                if (k <= wl) {
+                    const int sk = (k == wf && range_start(U, k, nwg) < S0) ? 2 * k + 1 : 2 * k;
+                    const int64_t row = (int64_t)sk * p.dec_rows_max + r;
+                    mlk[i] = *reinterpret_cast<const float2_t *>(p.ws_ml + 2 * row);
+                    ok[i] = *reinterpret_cast<const float4_t *>(p.ws_o + row * 128 + d0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CU; ++i) {
+                if (k0 + i > wl) break;
+                const float mk = mlk[i][0], lk = mlk[i][1];
+                const float mn = fmaxf(m, mk);
+                const float ms = mn == -INFINITY ? 0.0f : mn;
+                const float a = __builtin_amdgcn_exp2f(m - ms), c = __builtin_amdgcn_exp2f(mk - ms);
+                l = l * a + lk * c;
+                o = o * a + ok[i] * c;
+                m = mn;
+            }
+        }
+        const int j = r / p.G;
+        const int hq = h * p.G + (r - j * p.G);
+        const int64_t ob = (int64_t)(si.q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + d0;
+        const float inv = l > 0.f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out<ODT>(p.out, ob + i, o[i] * inv);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Prefill kernel: sequences with more than dec_rows_max packed rows.
 //
@@ -2034,6 +2090,12 @@ struct DecClass {
     size_t off_hdr, off_pre, off_ml, off_o;  // workspace layout
 };
 
+#ifndef GFA_COMB_FEW
+#define GFA_COMB_FEW 8          // resident decode workgroups per segment, at most
+#endif
+#ifndef GFA_COMB_FEW_KEYS
+#define GFA_COMB_FEW_KEYS 1024  // longest context for the per-segment merge
+#endif
 struct Plan {
     DecClass dc[2];
     int ndc;            // decode classes launched (0..2)
@@ -2046,6 +2108,7 @@ struct Plan {
     size_t off_items, off_split, off_pml, off_po, off_tbase;
     size_t bytes;       // the regions a call needs; the tile images follow at `bytes`
     size_t img_bytes;   // room the tile images of the call's shape can take (capped)
+    bool comb_short;    // contexts of at most GFA_COMB_FEW_KEYS keys (combine choice)
 };
 
 // Workspace room for the prefill tile images, at most (bytes).  A call whose
@@ -2158,7 +2221,7 @@ void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_h
 
 Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int max_query_len,
                int64_t max_seq_len, bool allow_split = true) {
-    Plan pl;
+    Plan pl{};
     const int G = num_heads / num_kv_heads;
     const int max_rows = max_query_len * G;
     const bool uniform = (int64_t)num_tokens == (int64_t)num_seqs * max_query_len;
@@ -2175,6 +2238,7 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     }
     pl.need_prefill = max_rows > (pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0);
     plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split, max_seq_len, max_query_len);
+    pl.comb_short = max_seq_len <= GFA_COMB_FEW_KEYS;
     return pl;
 }
 
@@ -2186,7 +2250,7 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
 // regions are monotone in all of these, and a call's classes are a subset of
 // these classes in the same order.
 Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num_kv_heads, bool allow_split) {
-    Plan pl;
+    Plan pl{};
     const int G = num_heads / num_kv_heads;
     pl.ndc = 0;
     if (G <= 16) plan_add_class(pl, 1, 0, 16);
@@ -2217,7 +2281,15 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
         const int crow = max(1, min(max_query_len * p.G, c.rows_hi));
         if (c.nrg == 1) {
             attn_decode_kernel<1, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
-            attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
+            // short contexts with few pieces per segment at most (resident
+            // workgroups over segments): one merging workgroup per segment.
+            // There the merge launch is mostly workgroups that find their
+            // segment whole (32 x 32 keys, 48/8: 6.7 against 7.9 us per
+            // call); with long contexts the per-row launch measured faster.
+            if (pl.comb_short && (int64_t)c.nwg <= (int64_t)GFA_COMB_FEW * num_seqs * num_kv_heads)
+                attn_combine_few_kernel<ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(pd);
+            else
+                attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
         } else {
             if (c.rows_hi > 32) attn_decode_kernel<2, QDT, ODT, true><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
             else attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);

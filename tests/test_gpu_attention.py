@@ -454,6 +454,38 @@ def test_decode_many_short_sequences():
     _run_and_check(b)
 
 
+SHORT_SPLIT = [
+    # seq_lens, Hq, Hkv: contexts of at most 1024 keys, yet more decode
+    # workgroups than segments, so segments are split and merged
+    ("8 x 1000, 8/1", [1000] * 8, 8, 1),                       # per-row merge launch
+    ("16 mixed, 48/8", [1024, 700, 33, 512] * 4, 48, 8),       # per-segment merge launch
+    ("32 x 1000, 48/8", [1000] * 32, 48, 8),                   # per-segment merge launch
+]
+
+
+@pytest.mark.parametrize("case", SHORT_SPLIT, ids=[c[0] for c in SHORT_SPLIT])
+def test_decode_short_contexts_split(case):
+    """Decode batches whose contexts are all short (at most 1024 keys: the
+    merge of split segments then runs one workgroup per segment when the
+    resident workgroups are few per segment) but long enough that the
+    stream-K plan splits segments: the plan's workgroup count (header word 1
+    of the decode workspace) exceeds the segments, and the output matches
+    the oracle."""
+    need_gpu()
+    name, sl, hq, hkv = case
+    announce(f"decode short contexts split {name}")
+    b = W.build_batch(sl, [1] * len(sl), hq, hkv, seed=31 + len(sl))
+    kp, vp = b.planes()
+    ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len,
+                                                          b.max_seq_len), b.device)
+    out = gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t, b.max_query_len,
+                                    b.max_seq_len, b.scale, workspace=ws, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    u, nwg = ws[:16].view(torch.int64).cpu().tolist()
+    assert nwg > len(sl) * hkv, (u, nwg)
+    assert_close(to_np_f32(out), batch_oracle(b))
+
+
 @pytest.mark.parametrize("nseq", [63, 64, 65])
 def test_decode_batch_size_boundary(nseq):
     """Batches on both sides of 64 sequences (the decode kernel locates its
