@@ -6,7 +6,8 @@ synchronisations between replays), and one replay against the oracle.  The
 attention path allocates nothing inside the C ABI, records no memset, and
 sizes its grids from host-fixed shapes only (CU count, num_seqs, heads,
 max_query_len), so the graph stays valid while the device-side metadata
-changes."""
+changes.  A prefill call that writes the tile images is captured and
+replayed the same way."""
 import math
 
 import numpy as np
@@ -97,3 +98,50 @@ def test_decode_step_graph_replay(heads, q_len, fused):
             ref = O.paged_attention_ref(q.float().cpu().numpy(), kh, vh, table, lens,
                                         qsl.cpu().numpy(), scale)
             assert_close(got.float().cpu().numpy(), ref)
+
+
+def test_prefill_with_tile_images_graph_replay():
+    """A prefill call whose plan writes the tile images (a 3000-token prompt
+    at 48/8: plan kernel, image pre-pass, prefill and split-merge launches)
+    captured once and replayed three times with new query values written in
+    place and eager calls in between; every replay equals the eager call bit
+    for bit, and the work-list header says the images were written."""
+    need_gpu()
+    import gfx906_fa_workloads as W
+    announce("graph replay prefill with tile images, 3000 tokens 48/8")
+    b = W.build_batch([3000], [3000], 48, 8, dtype="bf16", seed=81)
+    kp, vp = b.planes()
+    info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
+    ws = gfx906_fa.new_workspace(info["bytes"], b.device)
+    out = torch.empty((b.num_tokens, b.Hq, 128), dtype=torch.float32, device=DEV)
+
+    def call():
+        gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t, b.max_query_len,
+                                  b.max_seq_len, b.scale, out=out, workspace=ws)
+
+    call()
+    torch.cuda.synchronize()
+    hdr = ws[info["pf_header_offset"]:info["pf_header_offset"] + 16].view(torch.int32).cpu().tolist()
+    assert hdr[2] == 1 and hdr[3] > 0, hdr
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()  # warm-up on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gen = torch.Generator(device="cpu").manual_seed(82)
+    for it in range(3):
+        newq = torch.randn(b.query.shape, generator=gen, dtype=torch.float32).to(dtype=b.query.dtype, device=DEV)
+        b.query.copy_(newq)
+        call()  # eager reference, then the replay over the same inputs
+        torch.cuda.synchronize()
+        ref = out.clone()
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {it} differs from the eager call"
