@@ -63,6 +63,7 @@ struct AttnParams {
     const uint16_t *mask;             // optional additive fp16 mask [B][n_q][mask_cols]
     int64_t mask_bs, mask_rs;         // its batch and row strides (elements)
     int mask_cols;                    // keys it covers
+    int mask_vec;                     // rows 8-byte aligned, mask_cols % 4 == 0: 4 keys per load
     const int32_t *bt;
     int64_t bt_stride;
     const int32_t *seq_lens, *qsl, *q_abs;
@@ -1540,14 +1541,30 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
         const int kbase_t = PF_TK * (kt + ktb);
         if constexpr (MASK) {  // S' += mask[s][j][key] (natural log units -> log2)
             const uint16_t *mrow = p.mask + (int64_t)s * p.mask_bs + (int64_t)j * p.mask_rs;
+            if (p.mask_vec) {  // uniform: the lane's keys come in runs of 4 (register e = 4q + i)
 #pragma unroll
-            for (int st = 0; st < PF_NST; ++st)
+                for (int st = 0; st < PF_NST; ++st)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int key = kbase_t + 32 * st + 8 * (e >> 2) + 4 * hb + (e & 3);
-                    const float mv = key < p.mask_cols ? half_bits_to_f32(mrow[key]) : 0.0f;
-                    sacc[st][e] = fmaf(mv, LOG2E, sacc[st][e]);
-                }
+                    for (int q = 0; q < 4; ++q) {
+                        const int key = kbase_t + 32 * st + 8 * q + 4 * hb;  // a multiple of 4
+                        uint2 w = {0u, 0u};
+                        if (key < p.mask_cols) w = *reinterpret_cast<const uint2 *>(mrow + key);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint16_t hb16 = (uint16_t)((i < 2 ? w.x : w.y) >> (16 * (i & 1)));
+                            sacc[st][4 * q + i] = fmaf(half_bits_to_f32(hb16), LOG2E, sacc[st][4 * q + i]);
+                        }
+                    }
+            } else {
+#pragma unroll
+                for (int st = 0; st < PF_NST; ++st)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int key = kbase_t + 32 * st + 8 * (e >> 2) + 4 * hb + (e & 3);
+                        const float mv = key < p.mask_cols ? half_bits_to_f32(mrow[key]) : 0.0f;
+                        sacc[st][e] = fmaf(mv, LOG2E, sacc[st][e]);
+                    }
+            }
         }
         if (kbase_t + PF_TK - 1 > lim_min) {  // uniform: tile crosses some row's bound
 #pragma unroll
@@ -2664,6 +2681,8 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_tiled(
     p.mask_bs = mask_batch_stride;
     p.mask_rs = mask_row_stride;
     p.mask_cols = mask_cols;
+    p.mask_vec = mask != nullptr && ((uintptr_t)mask & 7) == 0 && (mask_batch_stride & 3) == 0 &&
+                 (mask_row_stride & 3) == 0 && (mask_cols & 3) == 0;
     p.Hkv = num_kv_heads;
     p.G = num_heads / num_kv_heads;
     p.block_size = block_size;

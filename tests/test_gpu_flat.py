@@ -104,7 +104,8 @@ def test_forward_flat_rejects_bad_arguments():
 
 
 def test_forward_flat_mask():
-    """Materialised fp16 mask: a causal 0/-inf mask and a dense additive one."""
+    """Materialised fp16 mask: a causal 0/-inf mask and a dense additive one
+    (128 columns: four keys per load), and a dense one of 101 columns."""
     need_gpu()
     announce("forward mask B=2 Hq=8 Hkv=2 Sq=40 Skv=100")
     B, Hq, Hkv, Sq, Skv = 2, 8, 2, 40, 100
@@ -119,6 +120,13 @@ def test_forward_flat_mask():
                                 torch.from_numpy(v).to(DEV), 0.09, mask=torch.from_numpy(m).to(DEV))
         torch.cuda.synchronize()
         assert_close(out.cpu().numpy(), O.flat_attention_ref(q, kq, v, 0.09, mask=m))
+    # 101 columns (more than Skv, not a multiple of 4): the mask is read one
+    # element at a time instead of four keys per load
+    m = rng.standard_normal((B, Sq, 101)).astype(np.float16)
+    out = gfx906_fa.forward(torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV),
+                            torch.from_numpy(v).to(DEV), 0.09, mask=torch.from_numpy(m).to(DEV))
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), O.flat_attention_ref(q, kq, v, 0.09, mask=m))
     with pytest.raises(RuntimeError, match="mutually exclusive"):
         gfx906_fa.forward(torch.from_numpy(q).to(DEV), torch.from_numpy(kq).to(DEV), torch.from_numpy(v).to(DEV),
                           0.09, mask=torch.from_numpy(m).to(DEV), q_abs_offset=torch.from_numpy(qa).to(DEV))
