@@ -408,14 +408,17 @@ __device__ __forceinline__ void stream_range(WaveAcc<NRG> &acc, const AttnParams
 // invisible to it, and the caller waits for them itself (vmcnt; loads
 // complete in order, so any later vector-memory instruction only makes such
 // a wait stricter).  M0 holds the LDS address; its previous value is put
-// back.  NT: the nontemporal hint (bytes read once; as the register path's
-// K/V loads).
+// back.  An LDS DMA may not read M0 in the instruction right after an SALU
+// write of it (the compiler puts a wait state there for its own copies):
+// s_nop 0.  NT: the nontemporal hint (bytes read once; as the register
+// path's K/V loads).
 template <bool NT>
 __device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
     uint32_t saved;
     if constexpr (NT)
         asm volatile("s_mov_b32 %0, m0\n\t"
                      "s_mov_b32 m0, %2\n\t"
+                     "s_nop 0\n\t"
                      "global_load_lds_dwordx4 %1, off nt\n\t"
                      "s_mov_b32 m0, %0"
                      : "=&s"(saved)
@@ -424,6 +427,7 @@ __device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
     else
         asm volatile("s_mov_b32 %0, m0\n\t"
                      "s_mov_b32 m0, %2\n\t"
+                     "s_nop 0\n\t"
                      "global_load_lds_dwordx4 %1, off\n\t"
                      "s_mov_b32 m0, %0"
                      : "=&s"(saved)
@@ -1513,22 +1517,17 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     float16v_t sacc[PF_NST];  // S' of the tile between its two half-steps
     // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile (stage kst)
     auto qk = [&](const uint8_t *kst) __attribute__((always_inline)) {
-        // -m in all 16 accumulator registers, built once per tile and fed to
-        // the first MFMA of both chains as srcC: one register pair, then
-        // seven 64-bit copies of it (v_mov_b64; the compiler's own splat is
-        // 15 32-bit moves)
-        float16v_t msplat;
-        {
-            const uint64_t pr = ((uint64_t)__float_as_uint(-m_use) << 32) | __float_as_uint(-m_use);
-            u64x8_t sp;
-            sp[7] = pr;
-#pragma unroll
-            for (int e = 0; e < 7; ++e) asm volatile("v_mov_b64 %0, %1" : "=v"(sp[e]) : "v"(pr));
-            msplat = __builtin_bit_cast(float16v_t, sp);
-        }
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
-            sacc[st] = msplat;
+            {   // -m in all 16 accumulator registers, built as a 64-bit splat
+                // (the compiler then builds it once per tile and feeds it to
+                // the first MFMA of both chains as srcC)
+                const uint64_t pr = ((uint64_t)__float_as_uint(-m_use) << 32) | __float_as_uint(-m_use);
+                u64x8_t sp;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sp[e] = pr;
+                sacc[st] = __builtin_bit_cast(float16v_t, sp);
+            }
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
                 const half8_t a = *reinterpret_cast<const half8_t *>(kst + kread + 32 * st * PF_KPITCH + 32 * kk);
