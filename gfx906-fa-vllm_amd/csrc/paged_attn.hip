@@ -26,8 +26,10 @@
 // Query rows are GQA-packed: rows of one kv-head are r = j*G + gq (token j,
 // q-head h*G + gq), so one K/V stream serves all G query heads.
 //
-//   attn_decode_kernel   sequences with n_q*G <= 32 rows (decode, verify):
-//                        stream-K over all KV sub-pages, equal share per wave
+//   attn_decode_kernel   sequences with n_q*G <= 64 rows (decode, verify):
+//                        stream-K over all KV sub-pages, equal share per wave;
+//                        16-, 32- or 48-row tiles per wave, 64 rows in two
+//                        32-row chunks
 //   attn_prefill_kernel  sequences with more rows: 128-row workgroups share
 //                        K/V tiles dequantized to fp16 in LDS; 32x32x16 MFMA
 #include <atomic>
@@ -802,9 +804,10 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
 
-    // per wave: its merge rows, or (verify tiles) its LDS ring while it
-    // streams; rows past R only lengthen the slice for the ring
-    constexpr int RA = NRG == 2 ? cmax(R, (DEC_RING * DEC_RING_SLOT + 4 * 132 - 1) / (4 * 132)) : R;
+    // per wave: its merge rows (32 at most: 48-row tiles merge in two
+    // passes), or (verify tiles) its LDS ring while it streams; rows past R
+    // only lengthen the slice for the ring
+    constexpr int RA = NRG >= 2 ? cmax(R < 32 ? R : 32, (DEC_RING * DEC_RING_SLOT + 4 * 132 - 1) / (4 * 132)) : R;
     __shared__ float sm_o[DEC_NW][RA][128 + 4];
     __shared__ float sm_m[DEC_NW][R], sm_l[DEC_NW][R];
     int64_t u = u0;
@@ -831,7 +834,7 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         load_rows<NRG, QDT>(p, h, si.q0, nrows, rc, si.sl, si.qa, i16, g, qf, lim);
         WaveAcc<NRG> acc;
         acc_init(acc);
-        if constexpr (NRG == 2) {  // verify tiles: sub-pages staged through this wave's sm_o slice
+        if constexpr (NRG >= 2) {  // verify tiles: sub-pages staged through this wave's sm_o slice
             static_assert(sizeof(sm_o[0]) >= DEC_RING * DEC_RING_SLOT, "ring fits the wave's slice");
             stream_range_lds<NRG, DEC_RING>(acc, p, s, h, 16 * a, min(16 * b, si.kv_lim), qf, lim, lane, i16,
                                             g, j0, jstep, reinterpret_cast<uint8_t *>(&sm_o[wv][0][0]));
@@ -841,8 +844,18 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
                                                                      lane, i16, g, j0, jstep);
         }
         // ---- merge the chunk's waves' states in LDS ------------------------
+        // in passes of 32 rows (row groups 2*ps, 2*ps + 1): a wave's LDS
+        // slice holds 32 rows, so 48-row tiles take two passes
+        constexpr int NPASS = (R + 31) / 32;
+        static_assert(!CHUNK || NPASS == 1, "two-chunk tiles merge in one pass");
+        const bool whole = a == 0 && b == si.nsub;
+        const int slot = 2 * w + (first ? 0 : 1);
+        const int rows_c = CHUNK ? nrows : min(nrows, R);
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ++ps) {
 #pragma unroll
         for (int rg = 0; rg < NRG; ++rg) {
+            if ((rg >> 1) != ps) continue;
             const float l = xrow_sum(acc.l[rg]);
             const int r = 16 * rg + i16;
             if (g == 0) {
@@ -851,16 +864,15 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
             }
 #pragma unroll
             for (int mm = 0; mm < 8; ++mm)
-                *reinterpret_cast<float4_t *>(&sm_o[wv][r][16 * mm + 4 * g]) = acc.o[rg][mm];
+                *reinterpret_cast<float4_t *>(&sm_o[wv][r - 32 * ps][16 * mm + 4 * g]) = acc.o[rg][mm];
         }
         __syncthreads();
-        const bool whole = a == 0 && b == si.nsub;
-        const int slot = 2 * w + (first ? 0 : 1);
-        const int rows_c = CHUNK ? nrows : min(nrows, R);
-        for (int it = threadIdx.x; it < rows_c * 32; it += 64 * DEC_NW) {
+        const int r_hi = NPASS == 1 ? rows_c : min(rows_c, 32 * ps + 32);
+        for (int it = threadIdx.x + 32 * 32 * ps; it < r_hi * 32; it += 64 * DEC_NW) {
             const int r = it >> 5, d0 = (it & 31) * 4;
             const int ch = CHUNK ? r / R : 0;   // the row's chunk: waves ch*wpc .. ch*wpc + wpc - 1
             const int rl = r - ch * R;          // its row inside the chunk
+            const int ro = rl - 32 * ps;        // its row in the LDS slices
             const int k0 = ch * wpc;
             float mx = -INFINITY;
             for (int k = k0; k < k0 + wpc; ++k) mx = fmaxf(mx, sm_m[k][rl]);
@@ -870,7 +882,7 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
             for (int k = k0; k < k0 + wpc; ++k) {
                 const float wk = __builtin_amdgcn_exp2f(sm_m[k][rl] - ms);
                 l = fmaf(sm_l[k][rl], wk, l);
-                o += *reinterpret_cast<const float4_t *>(&sm_o[k][rl][d0]) * wk;
+                o += *reinterpret_cast<const float4_t *>(&sm_o[k][ro][d0]) * wk;
             }
             if (whole) {
                 const int j = r / p.G;
@@ -888,7 +900,8 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
                 }
             }
         }
-        __syncthreads();  // LDS reused by the next piece
+        __syncthreads();  // LDS reused by the next pass or piece
+        }
         };
         static_assert(DEC_NW == 4 && DEC_CHUNK_ROWS <= 2 * 32, "two row chunks of two waves each");
         if (CHUNK && nrows > R) {  // uniform: rows R..nrows-1 (nrows <= 2R) in the second chunk
@@ -2100,7 +2113,7 @@ __global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p)
 // takes every row count up to its bound.  Sequences above the largest bound
 // go to the prefill kernel, which handles any row count.
 struct DecClass {
-    int nrg;            // row groups per decode wave (1 or 2)
+    int nrg;            // row groups per decode wave (1, 2 or 3)
     int rows_lo, rows_hi;
     int nwg;            // decode workgroups (resident workgroups of the device)
     size_t off_hdr, off_pre, off_ml, off_o;  // workspace layout
@@ -2113,8 +2126,8 @@ struct DecClass {
 #define GFA_COMB_FEW_KEYS 1024  // longest context for the per-segment merge
 #endif
 struct Plan {
-    DecClass dc[2];
-    int ndc;            // decode classes launched (0..2)
+    DecClass dc[3];
+    int ndc;            // decode classes launched (0..3)
     int dec_rows_max;   // largest decode row bound (0: every sequence is prefill)
     bool need_prefill;
     int pf_items_max;   // bound on prefill row tiles (0: no work list)
@@ -2242,15 +2255,28 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     const int max_rows = max_query_len * G;
     const bool uniform = (int64_t)num_tokens == (int64_t)num_seqs * max_query_len;
     pl.ndc = 0;
-    // the two-row-group class takes up to DEC_CHUNK_ROWS rows in 32-row chunks
+    // tiles of 16, 32 or 48 rows per wave (one, two or three row groups);
+    // up to DEC_CHUNK_ROWS rows the two-row-group class takes in 32-row
+    // chunks.  A 48-row tile streams each sub-page once for all its rows
+    // and dequantizes it once; two 32-row chunks stream and dequantize it
+    // twice (6/1 heads, 8 x (131072 + 6): 69.5 against 88.5 us).
+    const bool rows48 = max_rows > 32 && max_rows <= 48;
     const int hi2 = max_rows <= 32 ? 32 : DEC_CHUNK_ROWS;
     if (max_rows <= 16) {
         plan_add_class(pl, 1, 0, 16);
     } else if (uniform) {
-        if (max_rows <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, 0, hi2);
+        if (rows48) plan_add_class(pl, 3, 0, 48);
+        else if (max_rows <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, 0, hi2);
     } else {
+        // mixed row counts: each sequence takes the smallest tile that
+        // holds its rows (one launch pair per class)
         if (G <= 16) plan_add_class(pl, 1, 0, 16);
-        if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, hi2);
+        if (rows48) {
+            if (G <= 32) plan_add_class(pl, 2, pl.ndc ? 16 : 0, 32);
+            plan_add_class(pl, 3, pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0, 48);
+        } else if (G <= DEC_CHUNK_ROWS) {
+            plan_add_class(pl, 2, pl.ndc ? 16 : 0, hi2);
+        }
     }
     pl.need_prefill = max_rows > (pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0);
     plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split, max_seq_len, max_query_len);
@@ -2261,16 +2287,18 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
 // A plan whose every workspace region is at least that of any make_plan()
 // call with num_seqs <= max_num_seqs and num_tokens <= max_num_tokens (any
 // max_query_len, any mix of decode and prefill sequences): each decode class
-// a call can have, at its largest row bound (16 rows; 64 for the two-row-group
-// class), and a prefill work list sized for max_num_tokens.  plan_finish's
-// regions are monotone in all of these, and a call's classes are a subset of
-// these classes in the same order.
+// a call can have, at its largest row bound (16 rows; 48 for the three-row-
+// group class; 64 for the two-row-group class, which also covers a call's
+// 32-row class), and a prefill work list sized for max_num_tokens.
+// plan_finish's regions are monotone in all of these, and the decode
+// regions a call lays out sum to at most those laid out here.
 Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num_kv_heads, bool allow_split) {
     Plan pl{};
     const int G = num_heads / num_kv_heads;
     pl.ndc = 0;
     if (G <= 16) plan_add_class(pl, 1, 0, 16);
-    if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? 16 : 0, DEC_CHUNK_ROWS);
+    if (G <= 48) plan_add_class(pl, 3, pl.ndc ? 16 : 0, 48);
+    if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0, DEC_CHUNK_ROWS);
     pl.need_prefill = true;
     plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, -1, max_num_tokens);
     return pl;
@@ -2306,6 +2334,9 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
                 attn_combine_few_kernel<ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(pd);
             else
                 attn_combine_kernel<1, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
+        } else if (c.nrg == 3) {
+            attn_decode_kernel<3, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
+            attn_combine_kernel<3, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
         } else {
             if (c.rows_hi > 32) attn_decode_kernel<2, QDT, ODT, true><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
             else attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);

@@ -157,7 +157,7 @@ def test_graph_support_and_workspace_bound():
             assert bound == gfx906_fa.workspace_bound(max_seqs, max_tokens, hq, hkv) > 0
             shapes = []
             for n in {1, max(1, max_seqs // 2), max_seqs}:
-                for mq in (1, 2, 5, 6, 16, 2048):
+                for mq in (1, 2, 5, 6, 7, 8, 16, 2048):
                     if n * mq <= max_tokens:
                         shapes.append((n, n * mq, mq))          # uniform
                         if n > 1:

@@ -145,6 +145,20 @@ def test_plan_info():
     assert (m["decode_classes"], m["dec_rows_max"], m["prefill"]) == (2, 64, 1)
     assert 0 < m["pf_header_offset"] < m["bytes"] and m["pf_header_offset"] % 256 == 0
     assert gfx906_fa.plan_info(1, 32768, 48, 8, 32768, 32768)["decode_classes"] == 0
+    # 33-48 rows: the three-row-group class (48-row tiles); 49-64 rows: the
+    # two-row-group class in 32-row chunks.  Mixed row counts up to 48 take
+    # one class per tile size (16, 32, 48 rows).
+    u36 = gfx906_fa.plan_info(8, 48, 6, 1, 6, 131078)        # 6 verify tokens at 6/1: 36 rows
+    assert (u36["decode_classes"], u36["dec_rows_max"], u36["prefill"]) == (1, 48, 0)
+    u64 = gfx906_fa.plan_info(3, 24, 8, 1, 8, 5000)          # 8 tokens at 8/1: 64 rows
+    assert (u64["decode_classes"], u64["dec_rows_max"], u64["prefill"]) == (1, 64, 0)
+    mix48 = gfx906_fa.plan_info(4, 18, 6, 1, 6, 3000)        # 5 + 6 + 1 + 6 tokens at 6/1
+    assert (mix48["decode_classes"], mix48["dec_rows_max"], mix48["prefill"]) == (3, 48, 0)
+    mix64 = gfx906_fa.plan_info(3, 14, 8, 1, 8, 5000)        # 1 + 5 + 8 tokens at 8/1
+    assert (mix64["decode_classes"], mix64["dec_rows_max"], mix64["prefill"]) == (2, 64, 0)
+    g40 = gfx906_fa.plan_info(3, 5, 40, 1, 3, 5000)          # G = 40, 1 + 1 + 3 tokens: 40 and 120 rows
+    assert (g40["decode_classes"], g40["dec_rows_max"], g40["prefill"]) == (1, 64, 1)
+    assert mix48["bytes"] <= gfx906_fa.workspace_bound(4, 18, 6, 1)
     with pytest.raises(RuntimeError):
         gfx906_fa.plan_info(1, 1, 6, 4, 1, 1)             # heads not divisible
 

@@ -66,7 +66,9 @@ def _compare(b, k_new, v_new, slots, q_abs=None, odt=torch.float16):
     ("verify-48", [3000, 20, 1200], [5] * 3, 48, 8, 16),
     ("two-classes", [900, 40, 33, 2000, 7], [1, 3, 1, 2, 3], 8, 1, 16),  # 8 and 24 rows
     ("long-split", [20000, 777, 12345], [1] * 3, 8, 1, 16),
-    ("verify-36-rows", [3000, 6, 1200, 17, 20000], [6] * 5, 6, 1, 16),  # 36 rows: 32-row chunks
+    ("verify-36-rows", [3000, 6, 1200, 17, 20000], [6] * 5, 6, 1, 16),  # 36 rows: 48-row tiles
+    ("verify-64-rows", [2500, 9, 4100], [8] * 3, 8, 1, 16),            # 64 rows: 32-row chunks
+    ("three-classes", [3000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # 30, 36 and 6 rows
 ])
 def test_fused_write_matches_separate_calls(case):
     need_gpu()
