@@ -64,6 +64,22 @@ def test_noalloc_decode_bitidentical(dt):
         assert torch.equal(out, ref), name
 
 
+def test_noalloc_48_row_tiles_bitidentical():
+    """6-token verify at 6/1 (36 rows: the 48-row class), then a smaller
+    batch mixing 5-, 6- and 1-token sequences (16-, 32- and 48-row classes in
+    one call): bit-identical to the workspace entry."""
+    need_gpu()
+    first = W.build_batch([9000, 40, 2500, 700], [6] * 4, 6, 1, seed=76)
+    second = W.build_batch([3000, 800, 1200], [5, 6, 1], 6, 1, seed=77)
+    for name, b in (("verify 4 x 6 tokens 6/1", first), ("mixed 5/6/1 tokens 6/1", second)):
+        announce(f"noalloc {name}")
+        ref = _with_workspace(b, torch.float32)
+        out = torch.full_like(ref, 3.0)
+        _noalloc(b, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), name
+
+
 def test_noalloc_prefill_and_mixed():
     """A prefix-cached chunk whose row tiles the workspace entry splits over
     the keys (its partials would not fit the scratch: unsplit here), then a
