@@ -2122,6 +2122,9 @@ struct DecClass {
 #ifndef GFA_COMB_FEW
 #define GFA_COMB_FEW 8          // resident decode workgroups per segment, at most
 #endif
+#ifndef GFA_COMB_SEGS
+#define GFA_COMB_SEGS 64        // segments from which a mixed batch's verify class merges per segment
+#endif
 #ifndef GFA_COMB_FEW_KEYS
 #define GFA_COMB_FEW_KEYS 1024  // longest context for the per-segment merge
 #endif
@@ -2340,7 +2343,10 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
         } else {
             if (c.rows_hi > 32) attn_decode_kernel<2, QDT, ODT, true><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
             else attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
-            attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
+            if (c.rows_lo > 0 && (int64_t)num_seqs * num_kv_heads >= GFA_COMB_SEGS)
+                attn_combine_few_kernel<ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(pd);
+            else
+                attn_combine_kernel<2, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
         }
     }
     if (pl.need_prefill) {

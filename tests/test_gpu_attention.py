@@ -165,6 +165,8 @@ def test_verify_more_rows_than_decode_tile():
     ("6 tokens 48/8 bs64", [2000, 6000, 333], [6] * 3, 48, 8, 64),
     ("mixed 1/5/8 tokens 8/1", [3000, 900, 2500, 70], [1, 5, 8, 5], 8, 1, 16),  # 16-row and chunked classes
     ("5 tokens 64/8", [4000, 12, 900], [5] * 3, 64, 8, 16),              # 40 rows per kv-head
+    # 96 segments: the verify class of a mixed batch merges one segment per workgroup
+    ("verify + chunk 48/8", [20000] * 8 + [3000, 50, 9000, 5000], [6] * 8 + [1, 1, 1, 300], 48, 8, 16),
 ])
 def test_verify_rows_33_to_64(case):
     """Speculative verify with num_speculative_tokens = 5 (6 query tokens, the
