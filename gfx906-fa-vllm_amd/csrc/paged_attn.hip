@@ -1012,9 +1012,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 }
 
 // The same merge for segments of few pieces (a batch whose resident
-// workgroups are few per segment): one workgroup per (sequence, kv-head),
-// thread t takes d-chunk t % 32 of rows t / 32, t / 32 + 8, ... and merges
-// the segment's pieces in order, the loads of up to 8 of them in flight.
+// workgroups are few per segment), and for the second decode class of a
+// mixed batch with many segments (mostly empty there; a per-row grid would
+// be mostly workgroups that find nothing): one workgroup per (sequence,
+// kv-head), thread t takes d-chunk t % 32 of rows t / 32, t / 32 + 8, ...
+// and merges the segment's pieces in order, the loads of up to 8 of them in
+// flight.
 template <int ODT>
 __global__ __launch_bounds__(256) void attn_combine_few_kernel(AttnParams p) {
     const int s = blockIdx.x, h = blockIdx.y;
