@@ -387,6 +387,21 @@ def test_full_size_verify_cfg5_48_8():
     _check_permutation_invariance(b, out, "cfg5 48/8")
 
 
+def test_full_size_verify_ngram_k5():
+    """The reference's n-gram verify step at full size: 8 x (131072 + 6)
+    cached tokens at 6/1, 6 tokens x 6 q-heads = 36 packed rows per
+    sequence (the 48-row decode class, each segment split over about 64
+    workgroups).  Every verify token of every sequence against the oracle;
+    the whole output is invariant under a page permutation
+    (scripts/start_vllm_fa_ngram.sh:35-39)."""
+    need_gpu()
+    b = W.build_cfg("cfg5k6", device=DEV)
+    info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
+    assert (info["decode_classes"], info["dec_rows_max"], info["prefill"]) == (1, 48, 0)
+    out = _run_and_check(b, rows=list(range(b.num_tokens)))
+    _check_permutation_invariance(b, out, "cfg5k6")
+
+
 def test_full_size_prefill_cfg3():
     """cfg3, 32K causal prefill at 48/8: one query token per 8 row tiles of
     256 packed rows (every 341st token), the first and last tokens and the
