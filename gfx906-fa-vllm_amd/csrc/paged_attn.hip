@@ -2125,6 +2125,9 @@ struct DecClass {
 #ifndef GFA_COMB_FEW
 #define GFA_COMB_FEW 8          // resident decode workgroups per segment, at most
 #endif
+#ifndef GFA_DEC_ROWS48_UNITS
+#define GFA_DEC_ROWS48_UNITS 8  // sub-pages per decode workgroup from which 33-48 rows take 48-row tiles
+#endif
 #ifndef GFA_COMB_SEGS
 #define GFA_COMB_SEGS 64        // segments from which a mixed batch's verify class merges per segment
 #endif
@@ -2266,7 +2269,13 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
     // chunks.  A 48-row tile streams each sub-page once for all its rows
     // and dequantizes it once; two 32-row chunks stream and dequantize it
     // twice (6/1 heads, 8 x (131072 + 6): 69.5 against 88.5 us).
-    const bool rows48 = max_rows > 32 && max_rows <= 48;
+    // Below about 8 sub-pages per workgroup (short contexts, few segments)
+    // the 48-row tile's fixed costs (a two-pass merge, spilled registers)
+    // outweigh the second chunk it saves: 8 x (2000 + 6) at 6/1 measured
+    // 21.1 against 19.7 us, 32 x (1000 + 6) at 48/8 39.8 against 41.5 us.
+    const int64_t units_est = (int64_t)num_seqs * num_kv_heads * ((max(max_seq_len, (int64_t)1) + 15) / 16);
+    const bool rows48 = max_rows > 32 && max_rows <= 48 &&
+                        units_est >= (int64_t)GFA_DEC_ROWS48_UNITS * device_cus() * 4 * DecCfg<2>::wpe / DEC_NW;
     const int hi2 = max_rows <= 32 ? 32 : DEC_CHUNK_ROWS;
     if (max_rows <= 16) {
         plan_add_class(pl, 1, 0, 16);

@@ -152,13 +152,18 @@ def test_plan_info():
     assert (u36["decode_classes"], u36["dec_rows_max"], u36["prefill"]) == (1, 48, 0)
     u64 = gfx906_fa.plan_info(3, 24, 8, 1, 8, 5000)          # 8 tokens at 8/1: 64 rows
     assert (u64["decode_classes"], u64["dec_rows_max"], u64["prefill"]) == (1, 64, 0)
-    mix48 = gfx906_fa.plan_info(4, 18, 6, 1, 6, 3000)        # 5 + 6 + 1 + 6 tokens at 6/1
+    mix48 = gfx906_fa.plan_info(4, 18, 6, 1, 6, 30000)       # 5 + 6 + 1 + 6 tokens at 6/1
     assert (mix48["decode_classes"], mix48["dec_rows_max"], mix48["prefill"]) == (3, 48, 0)
     mix64 = gfx906_fa.plan_info(3, 14, 8, 1, 8, 5000)        # 1 + 5 + 8 tokens at 8/1
     assert (mix64["decode_classes"], mix64["dec_rows_max"], mix64["prefill"]) == (2, 64, 0)
     g40 = gfx906_fa.plan_info(3, 5, 40, 1, 3, 5000)          # G = 40, 1 + 1 + 3 tokens: 40 and 120 rows
     assert (g40["decode_classes"], g40["dec_rows_max"], g40["prefill"]) == (1, 64, 1)
     assert mix48["bytes"] <= gfx906_fa.workspace_bound(4, 18, 6, 1)
+    # below 8 sub-pages per decode workgroup 33-48 rows stay in 32-row chunks
+    s36 = gfx906_fa.plan_info(8, 48, 6, 1, 6, 2006)          # 8 x (2000 + 6) at 6/1
+    assert (s36["decode_classes"], s36["dec_rows_max"], s36["prefill"]) == (1, 64, 0)
+    smix = gfx906_fa.plan_info(4, 18, 6, 1, 6, 3000)
+    assert (smix["decode_classes"], smix["dec_rows_max"], smix["prefill"]) == (2, 64, 0)
     with pytest.raises(RuntimeError):
         gfx906_fa.plan_info(1, 1, 6, 4, 1, 1)             # heads not divisible
 

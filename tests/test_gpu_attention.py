@@ -150,9 +150,10 @@ def test_spec_verify(heads):
 
 def test_verify_more_rows_than_decode_tile():
     """n_q*G = 48 > 32 rows: the three-row-group launch takes them in one
-    48-row tile per wave."""
+    48-row tile per wave (long enough contexts: at least 8 sub-pages per
+    workgroup)."""
     need_gpu()
-    b = W.build_batch([900, 40], [8, 8], 6, 1, seed=8)
+    b = W.build_batch([40000, 40], [8, 8], 6, 1, seed=8)
     _run_and_check(b)
 
 
@@ -161,7 +162,8 @@ def test_verify_more_rows_than_decode_tile():
     ("7 tokens 6/1", [5000, 300, 64], [7] * 3, 6, 1, 16),                 # 42 rows
     ("8 tokens 8/1", [2500, 9, 4100], [8] * 3, 8, 1, 16),                 # 64 rows
     ("64/1 heads", [700, 33, 3000], [1] * 3, 64, 1, 16),                  # G = 64: 64 rows
-    ("mixed 5/6 tokens", [3000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # 16-, 32- and 48-row classes
+    ("mixed 5/6 tokens", [30000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # 16-, 32- and 48-row classes
+    ("mixed 5/6 tokens short", [3000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # 16-row and chunked classes
     ("6 tokens 48/8 bs64", [2000, 6000, 333], [6] * 3, 48, 8, 64),
     ("mixed 1/5/8 tokens 8/1", [3000, 900, 2500, 70], [1, 5, 8, 5], 8, 1, 16),  # 16-row and chunked classes
     ("5 tokens 64/8", [4000, 12, 900], [5] * 3, 64, 8, 16),              # 40 rows per kv-head

@@ -68,7 +68,8 @@ def _compare(b, k_new, v_new, slots, q_abs=None, odt=torch.float16):
     ("long-split", [20000, 777, 12345], [1] * 3, 8, 1, 16),
     ("verify-36-rows", [3000, 6, 1200, 17, 20000], [6] * 5, 6, 1, 16),  # 36 rows: 48-row tiles
     ("verify-64-rows", [2500, 9, 4100], [8] * 3, 8, 1, 16),            # 64 rows: 32-row chunks
-    ("three-classes", [3000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # 30, 36 and 6 rows
+    ("three-classes", [30000, 800, 1200, 40], [5, 6, 1, 6], 6, 1, 16),  # 30, 36 and 6 rows
+    ("verify-36-rows-short", [900, 6, 120], [6] * 3, 6, 1, 16),          # 36 rows: 32-row chunks
 ])
 def test_fused_write_matches_separate_calls(case):
     need_gpu()

@@ -23,13 +23,16 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("fused", [False, True])
-@pytest.mark.parametrize("heads,q_len", [((48, 8), 1), ((6, 1), 5), ((6, 1), 6)])
-def test_decode_step_graph_replay(heads, q_len, fused):
-    """fused: the cache write folded into the attention call."""
+@pytest.mark.parametrize("heads,q_len,max_blocks", [((48, 8), 1, 48), ((6, 1), 5, 48), ((6, 1), 6, 48),
+                                                   ((6, 1), 6, 640)])
+def test_decode_step_graph_replay(heads, q_len, max_blocks, fused):
+    """fused: the cache write folded into the attention call.  6 tokens at
+    6/1 (36 rows) take two 32-row chunks at 768-token contexts and 48-row
+    tiles at 10240."""
     need_gpu()
     Hq, Hkv = heads
-    announce(f"graph replay heads={heads} q_len={q_len} fused={fused}")
-    B, bs, max_blocks = 8, 16, 48
+    announce(f"graph replay heads={heads} q_len={q_len} max_blocks={max_blocks} fused={fused}")
+    B, bs = 8, 16
     NB = B * max_blocks
     T = B * q_len
     scale = 1.0 / math.sqrt(128)

@@ -69,8 +69,8 @@ def test_noalloc_48_row_tiles_bitidentical():
     batch mixing 5-, 6- and 1-token sequences (16-, 32- and 48-row classes in
     one call): bit-identical to the workspace entry."""
     need_gpu()
-    first = W.build_batch([9000, 40, 2500, 700], [6] * 4, 6, 1, seed=76)
-    second = W.build_batch([3000, 800, 1200], [5, 6, 1], 6, 1, seed=77)
+    first = W.build_batch([40000, 40, 2500, 700], [6] * 4, 6, 1, seed=76)
+    second = W.build_batch([30000, 800, 1200], [5, 6, 1], 6, 1, seed=77)
     for name, b in (("verify 4 x 6 tokens 6/1", first), ("mixed 5/6/1 tokens 6/1", second)):
         announce(f"noalloc {name}")
         ref = _with_workspace(b, torch.float32)
