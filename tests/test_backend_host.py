@@ -175,8 +175,11 @@ def test_graph_support_and_workspace_bound():
                 T = rng.randint(n, max_tokens)
                 shapes.append((n, T, rng.randint(1, T - n + 1)))
             for n, T, mq in shapes:
-                need = gfx906_fa.workspace_size(n, T, hq, hkv, mq, 1 << 17)
-                assert need <= bound, (hq, hkv, max_seqs, max_tokens, n, T, mq, need, bound)
+                # long and short contexts: the decode classes differ (48-row
+                # tiles only with enough sub-pages per workgroup)
+                for msl in (1 << 17, 2048):
+                    need = gfx906_fa.workspace_size(n, T, hq, hkv, mq, msl)
+                    assert need <= bound, (hq, hkv, max_seqs, max_tokens, n, T, mq, msl, need, bound)
     # several layer shapes: the largest bound
     both = workspace_upper_bound(64, 4096, [(48, 8), (6, 1)])
     assert both == max(gfx906_fa.workspace_bound(64, 4096, 48, 8), gfx906_fa.workspace_bound(64, 4096, 6, 1))
