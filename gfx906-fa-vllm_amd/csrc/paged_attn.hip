@@ -90,13 +90,14 @@ struct AttnParams {
     // and writes the output.  nullptr: the prefill grid is
     // (row tiles * Hkv, num_seqs) instead, with no split.
     int *pf_seq, *pf_rt, *pf_kt0, *pf_kt1, *pf_slot, *pf_count;
+    int pf_rows;        // query rows per prefill row tile: PF_ROWS, or PF_ROWS / 2 (KS = 2 tiles)
     int pf_items_max;   // row tiles, at most
     int pf_grid_items;  // work-list capacity (the grid): row tiles + extra pieces
     int pf_ncu;         // CUs the split targets
     int pf_split_max;   // split row tiles, at most
     int pf_slots_max;   // partial slots per kv head
     int *pf_split;      // split row tiles: (sequence, row tile, first slot, pieces) each
-    float *pf_ml, *pf_o;  // partials: [slot][Hkv][PF_ROWS] x (m, l) and x 128
+    float *pf_ml, *pf_o;  // partials: [slot][Hkv][pf_rows] x (m, l) and x 128
     // Dequantized tile images (work-list launches only; nullptr: none): the
     // fp16 K^ and V^T of 64-key tile kt of prefill sequence s for kv-head h,
     // byte for byte the prefill kernel's LDS stages, at image
@@ -1113,10 +1114,23 @@ __global__ __launch_bounds__(256) void attn_combine_few_kernel(AttnParams p) {
 // grid (row_tiles * Hkv, num_seqs): blockIdx.x % Hkv is the kv-head (one head
 // per XCD when Hkv = 8: the XCD's L2 serves that head's K/V to all its
 // workgroups) and row tiles run last-first, heaviest causal ranges first.
+//
+// Key-interleaved 128-row tile (KS = 2).  With few rows per kv-head most of a
+// 256-row tile's consumer waves idle and a key tile costs a whole
+// QK -> softmax -> PV chain of one wave per SIMD, as long as a full tile.
+// The KS = 2 form gives consumer waves w and w + 4 the same 32 rows: group A
+// (waves 0-3) takes the even key tiles, group B (waves 4-7) the odd ones, so
+// one tile is consumed per half-step (A's QK beside B's softmax + PV on each
+// SIMD, and the reverse in the next half-step) and the producers dequantize a
+// whole tile (K^ of tile h + 1, V^T of tile h) per half-step h into two LDS
+// stages (tile t: stage t % 2, so group A always reads stage 0 and group B
+// stage 1).  The two partial states of each row merge through LDS at the
+// end: each wave of a pair sends the partner the half of O^T it will not
+// store.
 constexpr int PF_CWAVES = 8;                  // consumer waves (32 rows each)
 constexpr int PF_PWAVES = 4;                  // producer waves (one sub-page of each tile)
 constexpr int PF_WAVES = PF_CWAVES + PF_PWAVES;
-constexpr int PF_ROWS = 32 * PF_CWAVES;
+constexpr int PF_ROWS = 32 * PF_CWAVES;       // rows per tile (KS = 1); KS = 2 tiles hold PF_ROWS / 2
 constexpr int PF_TK = 64;                     // keys per LDS tile
 constexpr int PF_NSP = PF_TK / 16;            // sub-pages per tile
 static_assert(PF_NSP == PF_PWAVES, "one producer wave per sub-page");
@@ -1256,12 +1270,15 @@ __device__ __forceinline__ void pf_dequant_v(const PfRaw &r, uint8_t *vst, int s
     }
 }
 
-template <int QDT, int ODT, bool VF16, bool MASK>
+template <int QDT, int ODT, bool VF16, bool MASK, int KS = 1>
 __global__ __launch_bounds__(64 * PF_WAVES)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p) {
-    // three LDS stages of K^ and of V^T (tile t in stage t % 3)
-    __shared__ __attribute__((aligned(16))) uint8_t ldsk[PF_NSTAGE * PF_KBYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t ldsv[PF_NSTAGE * PF_VBYTES];
+    static_assert(KS == 1 || KS == 2, "256-row tiles, or 128-row key-interleaved tiles");
+    constexpr int ROWS = PF_ROWS / KS;               // query rows per tile
+    constexpr int NSTAGE = KS == 1 ? PF_NSTAGE : 2;  // LDS stages of K^ and of V^T (tile t: t % NSTAGE)
+    __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * (PF_KBYTES + PF_VBYTES)];
+    uint8_t *const ldsk = lds;
+    uint8_t *const ldsv = lds + NSTAGE * PF_KBYTES;
     const int Hkv = p.Hkv;
     const int h = blockIdx.x % Hkv;
     int s, rt, kt0 = 0, kt1 = INT32_MAX, slot = -1;
@@ -1281,13 +1298,13 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     const int nq = p.qsl[s + 1] - q0;
     const int nrows = nq * p.G;
     if (nq <= 0 || nrows <= p.dec_rows_max) return;  // uniform over the workgroup
-    const int row0 = PF_ROWS * rt;
+    const int row0 = ROWS * rt;
     if (row0 >= nrows) return;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int sl = p.seq_lens[s];
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int jlast = (min(row0 + PF_ROWS, nrows) - 1) / p.G;
+    const int jlast = (min(row0 + ROWS, nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
     // key tiles [ktb, ktb + ntk) of the row tile's (kv_end + PF_TK - 1) / PF_TK;
     // the loops below count tiles from 0 and add ktb where they need a key index
@@ -1304,7 +1321,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
         // cbase + 64 + i).  Tile t sits in ring slot t % PF_PDEPTH from its
         // fetch until its dequant, one iteration before the consumers read it.
         const int wsp = w - PF_CWAVES;
-        if (p.pf_tiles != nullptr && p.pf_count[2] != 0) {  // uniform
+        // (no images for KS = 2 tiles: the host never passes them there)
+        if (KS == 1 && p.pf_tiles != nullptr && p.pf_count[2] != 0) {  // uniform
             // The tiles are dequantized images in the workspace.  Copy batch
             // b (K^ of tile b/2 for even b, V^T for odd b) goes from the image
             // straight into its LDS stage in half-step b - 4 and has landed by
@@ -1399,20 +1417,77 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
                 ready(pw1);
             }
         };
-        // dequantizes the K (or V) half of tile t (in the ring) into stage t % 3
+        // dequantizes the K (or V) half of tile t (in the ring) into stage t % NSTAGE
         auto dequant_k = [&](const PfRawT &rw, int t) __attribute__((always_inline)) {
-            uint8_t *kst = ldsk + (t % PF_NSTAGE) * PF_KBYTES;
+            uint8_t *kst = ldsk + (t % NSTAGE) * PF_KBYTES;
             pf_dequant_k(rw.h[0], kst, wsp, lane, 0, p.pf_kmul);
             pf_dequant_k(rw.h[1], kst, wsp, lane, 1, p.pf_kmul);
         };
         auto dequant_v = [&](const PfRawT &rw, int t, auto tail) __attribute__((always_inline)) {
-            uint8_t *vst = ldsv + (t % PF_NSTAGE) * PF_VBYTES;
+            uint8_t *vst = ldsv + (t % NSTAGE) * PF_VBYTES;
             constexpr bool T = decltype(tail)::value;
             pf_dequant_v<T, VF16>(rw.h[0], vst, wsp, lane, 0);
             pf_dequant_v<T, VF16>(rw.h[1], vst, wsp, lane, 1);
         };
         using NoTail = std::integral_constant<bool, false>;
         using IsTail = std::integral_constant<bool, true>;
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1 % PF_PDEPTH>;
+        using S2 = std::integral_constant<int, 2 % PF_PDEPTH>;
+        using S3 = std::integral_constant<int, 3 % PF_PDEPTH>;
+        if constexpr (KS == 2) {
+            // Half-steps h = 0 .. ntk (a barrier each, after the prologue's):
+            // K^ of tile h + 1 and V^T of tile h are written in half-step h
+            // (K^ of tile 0 in the prologue).  The K stage (h + 1) % 2 was
+            // last read by the QK of tile h - 1 and the V stage h % 2 by the
+            // softmax + PV of tile h - 2, both in half-step h - 1.  After V^T
+            // of tile h its ring slot takes tile h + PF_PDEPTH.
+            static_assert(KS != 2 || PF_PDEPTH == 4, "the KS = 2 producer loop is unrolled for a 4-deep ring");
+            if (ntk > 0) {
+                pw0 = load_pg(0);
+                pw1 = ntk > 64 ? load_pg(1) : 0;
+                ready(pw0);
+                ready(pw1);
+#pragma unroll
+                for (int i = 0; i < PF_PDEPTH; ++i) fetch(ring[i], i);
+                dequant_k(ring[0], 0);
+            }
+            __syncthreads();
+            // a half-step h < ntk - 1: tile h + 1 in slot SK, tile h in slot SV
+            auto hs2 = [&](int hh, auto sv_c, auto sk_c) __attribute__((always_inline)) {
+                constexpr int SV = decltype(sv_c)::value, SK = decltype(sk_c)::value;
+                dequant_k(ring[SK], hh + 1);
+                dequant_v(ring[SV], hh, NoTail{});
+                fetch(ring[SV], hh + PF_PDEPTH);
+                __syncthreads();
+            };
+            int hh = 0;
+            for (; hh + PF_PDEPTH <= ntk - 1; hh += PF_PDEPTH) {
+                slide(hh);
+                hs2(hh, S0{}, S1{});
+                hs2(hh + 1, S1{}, S2{});
+                hs2(hh + 2, S2{}, S3{});
+                hs2(hh + 3, S3{}, S0{});
+            }
+            slide(hh);
+            const int rem = ntk - 1 - hh;  // half-steps left before the tail one: 0 .. 3 (uniform)
+            if (rem >= 1) hs2(hh, S0{}, S1{});
+            if (rem >= 2) hs2(hh + 1, S1{}, S2{});
+            if (rem >= 3) hs2(hh + 2, S2{}, S3{});
+            if (ntk >= 1) {  // half-step ntk - 1: V^T of the tail tile, from slot (ntk - 1) % 4
+                const int tl = ntk - 1;
+                switch (tl % PF_PDEPTH) {
+                case 0: dequant_v(ring[0], tl, IsTail{}); break;
+                case 1: dequant_v(ring[1 % PF_PDEPTH], tl, IsTail{}); break;
+                case 2: dequant_v(ring[2 % PF_PDEPTH], tl, IsTail{}); break;
+                default: dequant_v(ring[3 % PF_PDEPTH], tl, IsTail{}); break;
+                }
+                __syncthreads();
+            }
+            __syncthreads();  // half-step ntk: no producer work
+            __syncthreads();  // the consumers' merge exchange
+            return;
+        }
         if (ntk > 0) {
             pw0 = load_pg(0);
             pw1 = ntk > 64 ? load_pg(1) : 0;
@@ -1439,10 +1514,6 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
             fetch(ring[SL], t + PF_PDEPTH);
             __syncthreads();
         };
-        using S0 = std::integral_constant<int, 0>;
-        using S1 = std::integral_constant<int, 1 % PF_PDEPTH>;
-        using S2 = std::integral_constant<int, 2 % PF_PDEPTH>;
-        using S3 = std::integral_constant<int, 3 % PF_PDEPTH>;
         // tiles 1 .. ntk - 2 (full), then the tail tile ntk - 1
         int t = 1;
         for (; t + PF_PDEPTH <= ntk - 1; t += PF_PDEPTH) {
@@ -1478,17 +1549,20 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
 
     // ---- consumer: 32 query rows ----------------------------------------
     const int hb = lane >> 5;
+    // the wave's 32-row chunk of the tile and its group (A: 0, B: 1)
+    const int cw = KS == 1 ? w : w % (PF_CWAVES / 2);
+    const int grp = w / (PF_CWAVES / 2);
     // this lane's query row, its causal bound and its Q^T fragments
-    const int r = row0 + 32 * w + (lane & 31);
+    const int r = row0 + 32 * cw + (lane & 31);
     const bool rvalid = r < nrows;
     const int j = rvalid ? r / p.G : 0;
     const int hq = h * p.G + (rvalid ? r - j * p.G : 0);
     const int lim = rvalid ? (p.causal ? min(sl - 1, qa + j) : sl - 1) : INT32_MAX;
-    const bool wact = row0 + 32 * w < nrows;  // uniform over the wave
+    const bool wact = row0 + 32 * cw < nrows;  // uniform over the wave (and its KS = 2 partner)
     if (!wact) {
         // all 32 rows past the sequence's rows (its last row tile): keep the
         // workgroup's barrier count
-        for (int i = 0; i < 2 * ntk + 2; ++i) __syncthreads();
+        for (int i = 0; i < (KS == 1 ? 2 * ntk + 2 : ntk + 3); ++i) __syncthreads();
         return;
     }
     half8_t qf[8];
@@ -1641,50 +1715,118 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
         l_run += tsum;
     };
     __syncthreads();  // the producers' first tile
-    const bool grp_b = w >= PF_CWAVES / 2;  // uniform over the wave
-    if (grp_b) __syncthreads();  // half-step 0
-    for (int kt = 0, stg = 0; kt < ntk; ++kt, stg = stg == PF_NSTAGE - 1 ? 0 : stg + 1) {
-        qk(ldsk + stg * PF_KBYTES);
-        __syncthreads();
-        sv(kt, ldsv + stg * PF_VBYTES);
-        __syncthreads();
+    if constexpr (KS == 1) {
+        if (grp) __syncthreads();  // half-step 0
+        for (int kt = 0, stg = 0; kt < ntk; ++kt, stg = stg == NSTAGE - 1 ? 0 : stg + 1) {
+            qk(ldsk + stg * PF_KBYTES);
+            __syncthreads();
+            sv(kt, ldsv + stg * PF_VBYTES);
+            __syncthreads();
+        }
+        if (!grp) __syncthreads();  // half-step 2 ntk (group B's last softmax)
+    } else {
+        // group A: the even tiles (QK in half-step kt, softmax + PV in kt + 1)
+        // from stage 0; group B: the odd tiles from stage 1.  Both then pad
+        // to the ntk + 2 barriers of the producers' half-steps.
+        if (grp) __syncthreads();  // half-step 0
+        const uint8_t *kst = ldsk + grp * PF_KBYTES;
+        const uint8_t *vst = ldsv + grp * PF_VBYTES;
+        for (int kt = grp; kt < ntk; kt += 2) {
+            qk(kst);
+            __syncthreads();
+            sv(kt, vst);
+            __syncthreads();
+        }
+        if ((ntk & 1) == grp) __syncthreads();
     }
-    if (!grp_b) __syncthreads();  // half-step 2 ntk (group B's last softmax)
 
     // normalise and store: register e of d-tile dt is d = 32dt + 8(e/4) + 4hb + e%4
-    {
-        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-        const float l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    float l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    float mrow = has_m ? m_use : -INFINITY;
+    using D0 = std::integral_constant<int, 0>;
+    using D2 = std::integral_constant<int, 2>;
+    if constexpr (KS == 2) {
+        // Merge the pair's partial states through LDS (the stages are free:
+        // every read of them ended before the last barrier).  Group A stores
+        // d-tiles 0-1 and sends 2-3, group B the reverse; both send (m, l).
+        // Layout [group][chunk][8 float4][64 lanes]: a wave's 16-byte stores
+        // and loads are lane-contiguous.
+        float4_t *xo = reinterpret_cast<float4_t *>(lds);
+        float2_t *xml = reinterpret_cast<float2_t *>(lds + 2 * 4 * 8 * 64 * 16);
+        static_assert(2 * 4 * 8 * 64 * 16 + 2 * 4 * 64 * 8 <= NSTAGE * (PF_KBYTES + PF_VBYTES), "merge fits the stages");
+        float4_t *mine = xo + (grp * 4 + cw) * 8 * 64 + lane;
+        auto send = [&](auto dtb) __attribute__((always_inline)) {
+            constexpr int DB = decltype(dtb)::value;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                    mine[(4 * i + q4) * 64] = float4_t{o[DB + i][4 * q4], o[DB + i][4 * q4 + 1], o[DB + i][4 * q4 + 2],
+                                                       o[DB + i][4 * q4 + 3]};
+        };
+        if (grp == 0) send(D2{});
+        else send(D0{});
+        xml[(grp * 4 + cw) * 64 + lane] = float2_t{mrow, l};
+        __syncthreads();
+        const float4_t *theirs = xo + ((1 - grp) * 4 + cw) * 8 * 64 + lane;
+        const float2_t mlp = xml[((1 - grp) * 4 + cw) * 64 + lane];
+        const float M = fmaxf(mrow, mlp[0]);
+        const bool none = M == -INFINITY;  // neither half saw a key of this row
+        const float a = none ? 0.0f : __builtin_amdgcn_exp2f(mrow - M);
+        const float b = none ? 0.0f : __builtin_amdgcn_exp2f(mlp[0] - M);
+        auto merge = [&](auto dtb) __attribute__((always_inline)) {
+            constexpr int DB = decltype(dtb)::value;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4_t t = theirs[(4 * i + q4) * 64];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) o[DB + i][4 * q4 + k] = fmaf(o[DB + i][4 * q4 + k], a, t[k] * b);
+                }
+        };
+        if (grp == 0) merge(D0{});
+        else merge(D2{});
+        l = fmaf(l, a, mlp[1] * b);
+        mrow = M;
+    }
+    // stores d-tiles DB .. DB + ND - 1 of the wave's rows
+    auto store_tiles = [&](auto dtb, auto ndt) __attribute__((always_inline)) {
+        constexpr int DB = decltype(dtb)::value, ND = decltype(ndt)::value;
         if (slot >= 0) {  // a piece of a split row tile: unnormalised O, m (log2), l
-            const int rl = 32 * w + (lane & 31);
+            const int rl = 32 * cw + (lane & 31);
             if (!rvalid) return;  // the combine reads the sequence's rows only
             const int64_t reg = (int64_t)slot * Hkv + h;
-            float *po = p.pf_o + (reg * PF_ROWS + rl) * 128 + 4 * hb;
+            float *po = p.pf_o + (reg * ROWS + rl) * 128 + 4 * hb;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int dt = DB; dt < DB + ND; ++dt)
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4)
                     *reinterpret_cast<float4_t *>(po + 32 * dt + 8 * q4) =
                         float4_t{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
-            if (hb == 0) {
-                float *pm = p.pf_ml + (reg * PF_ROWS + rl) * 2;
-                pm[0] = has_m ? m_use : -INFINITY;
+            if (DB == 0 && hb == 0) {
+                float *pm = p.pf_ml + (reg * ROWS + rl) * 2;
+                pm[0] = mrow;
                 pm[1] = l;
             }
         } else if (rvalid) {
             const float inv = l > 0.f ? 1.0f / l : 0.0f;
             const int64_t ob = (int64_t)(q0 + j) * p.o_ts + (int64_t)hq * p.o_hs + 4 * hb;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int dt = DB; dt < DB + ND; ++dt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
                     store_out<ODT>(p.out, ob + 32 * dt + 8 * (e >> 2) + (e & 3), o[dt][e] * inv);
         }
-    }
+    };
+    if constexpr (KS == 1) store_tiles(D0{}, std::integral_constant<int, 4>{});
+    else if (grp == 0) store_tiles(D0{}, D2{});
+    else store_tiles(D2{}, D2{});
 }
 
 // ---------------------------------------------------------------------------
-// Prefill work list.  One workgroup enumerates every (sequence, 256-row tile)
+// Prefill work list.  One workgroup enumerates every (sequence, row tile)
 // of prefill work and counting-sorts the items by the number of 64-key tiles
 // their causal range spans, heaviest first, so that the prefill grid
 // dispatches the longest workgroups first whatever the order of the
@@ -1728,7 +1870,7 @@ __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
 __device__ __forceinline__ int pl_tiles(const AttnParams &p, int s) {
     const int nq = p.qsl[s + 1] - p.qsl[s];
     const int nrows = nq * p.G;
-    return (nq > 0 && nrows > p.dec_rows_max) ? (nrows + PF_ROWS - 1) / PF_ROWS : 0;
+    return (nq > 0 && nrows > p.dec_rows_max) ? (nrows + p.pf_rows - 1) / p.pf_rows : 0;
 }
 
 // 64-key tiles row tile rt of sequence s attends (the prefill kernel's ntk_all)
@@ -1738,7 +1880,7 @@ __device__ __forceinline__ int pl_ntk(const AttnParams &p, int s, int rt) {
     const int nrows = nq * p.G;
     const int sl = p.seq_lens[s];
     const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int jlast = (min(PF_ROWS * (rt + 1), nrows) - 1) / p.G;
+    const int jlast = (min(p.pf_rows * (rt + 1), nrows) - 1) / p.G;
     const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
     return (kv_end + PF_TK - 1) / PF_TK;
 }
@@ -2035,14 +2177,15 @@ template <int ODT>
 __global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p) {
     constexpr int RPU = 16, U = 4;
     const int nsplit = p.pf_count[1];
-    const int units = nsplit * p.Hkv * (PF_ROWS / RPU);
+    const int prows = p.pf_rows;
+    const int units = nsplit * p.Hkv * (prows / RPU);
     const int rr = threadIdx.x >> 5, d = 4 * (threadIdx.x & 31);
-    const int64_t rstep = (int64_t)p.Hkv * PF_ROWS;  // piece c -> c + 1
+    const int64_t rstep = (int64_t)p.Hkv * prows;  // piece c -> c + 1
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         const int h = u % p.Hkv;
         const int t = u / p.Hkv;
-        const int rg = t % (PF_ROWS / RPU);
-        const int *e = p.pf_split + 4 * (t / (PF_ROWS / RPU));
+        const int rg = t % (prows / RPU);
+        const int *e = p.pf_split + 4 * (t / (prows / RPU));
         const int s = e[0], rt = e[1], slot0 = e[2], k = e[3];
         const int q0 = p.qsl[s];
         const int nrows = (p.qsl[s + 1] - q0) * p.G;
@@ -2053,8 +2196,8 @@ __global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p)
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int rl = RPU * rg + rr + 8 * i;  // row inside the tile
-            ok[i] = PF_ROWS * rt + rl < nrows;
-            reg0[i] = ((int64_t)slot0 * p.Hkv + h) * PF_ROWS + rl;
+            ok[i] = prows * rt + rl < nrows;
+            reg0[i] = ((int64_t)slot0 * p.Hkv + h) * prows + rl;
             M[i] = -INFINITY;
             L[i] = 0.f;
             acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -2090,7 +2233,7 @@ __global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p)
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             if (!ok[i]) continue;
-            const int r = PF_ROWS * rt + RPU * rg + rr + 8 * i;
+            const int r = prows * rt + RPU * rg + rr + 8 * i;
             const float inv = L[i] > 0.f ? 1.0f / L[i] : 0.0f;
             const int j = r / p.G;
             const int hq = h * p.G + (r - j * p.G);
@@ -2134,11 +2277,15 @@ struct DecClass {
 #ifndef GFA_COMB_FEW_KEYS
 #define GFA_COMB_FEW_KEYS 1024  // longest context for the per-segment merge
 #endif
+#ifndef GFA_PF_KS2_MAX_ROWS
+#define GFA_PF_KS2_MAX_ROWS 128  // most rows per kv-head for which 128-row (KS = 2) prefill tiles are chosen
+#endif
 struct Plan {
     DecClass dc[3];
     int ndc;            // decode classes launched (0..3)
     int dec_rows_max;   // largest decode row bound (0: every sequence is prefill)
     bool need_prefill;
+    int pf_rows;        // rows per prefill row tile: PF_ROWS (KS = 1) or PF_ROWS / 2 (KS = 2)
     int pf_items_max;   // bound on prefill row tiles (0: no work list)
     int pf_split_max;   // split row tiles, at most
     int pf_slots_max;   // partial slots per kv head
@@ -2207,9 +2354,9 @@ void plan_add_class(Plan &pl, int nrg, int lo, int hi) {
 void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_heads, bool force_pf,
                  bool allow_split, int64_t max_seq_len, int64_t max_query_len) {
     pl.dec_rows_max = pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0;
-    // row tiles over all sequences <= sum ceil(n_q * G / 256) <= T*G/256 + B
+    // row tiles over all sequences <= sum ceil(n_q * G / R) <= T*G/R + B (R = pf_rows)
     const int pf_seqs = min(num_seqs, PL_MAX_SEQS);
-    const int64_t items = (max(num_tokens, (int64_t)0) * G + PF_ROWS - 1) / PF_ROWS + pf_seqs;
+    const int64_t items = (max(num_tokens, (int64_t)0) * G + pl.pf_rows - 1) / pl.pf_rows + pf_seqs;
     // a split row tile holds more than pf_ncu / Hkv of the launch's key tiles:
     // fewer than ceil(CUs / Hkv) of them, with fewer than twice that many pieces
     // (a few row tiles, n <= 2 ceil(CUs / Hkv), may instead be cut into up to
@@ -2235,6 +2382,7 @@ void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_h
     pl.off_items = off;
     // work list: a 256-byte header (item count, split row tile count), the
     // five item arrays, the split list, then the partials of the split pieces
+    // (slots of PF_ROWS rows, which also hold the PF_ROWS / 2 of KS = 2 tiles)
     pl.off_split = pl.off_items + 256 + align256((size_t)5 * grid_items * sizeof(int));
     const size_t prow = (size_t)pl.pf_slots_max * num_kv_heads * PF_ROWS;
     pl.off_pml = pl.off_split + align256((size_t)4 * pl.pf_split_max * sizeof(int));
@@ -2294,6 +2442,16 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
         }
     }
     pl.need_prefill = max_rows > (pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0);
+    // Prefill tile rows: 128-row key-interleaved (KS = 2) tiles when the
+    // longest prefill sequence has at most 128 rows per kv-head.  There a
+    // 256-row tile fills at most half its consumer waves and costs about as
+    // much per key tile as a full one.  Measured on one box (48/8, fp16 out):
+    // 8 x (32768 + 12) 201 -> 193 us, 32 x (4096 + 12) 104.6 -> 98.2 us,
+    // 8 x (32768 + 16) at 64/8 222 -> 216 us.  With more rows the extra row
+    // tiles cost more than the padding they save: 1 x (65536 + 50) (300
+    // rows, three 128-row tiles against two of 256) 148.5 -> 152.7 us,
+    // 1 x (131072 + 64) (384 rows) 261 -> 275 us.
+    pl.pf_rows = max_rows <= GFA_PF_KS2_MAX_ROWS ? PF_ROWS / 2 : PF_ROWS;
     plan_finish(pl, num_seqs, num_tokens, G, num_kv_heads, false, allow_split, max_seq_len, max_query_len);
     pl.comb_short = max_seq_len <= GFA_COMB_FEW_KEYS;
     return pl;
@@ -2315,6 +2473,7 @@ Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num
     if (G <= 48) plan_add_class(pl, 3, pl.ndc ? 16 : 0, 48);
     if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0, DEC_CHUNK_ROWS);
     pl.need_prefill = true;
+    pl.pf_rows = PF_ROWS / 2;  // the smaller tile: the most row tiles
     plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, -1, max_num_tokens);
     return pl;
 }
@@ -2367,9 +2526,10 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
         // at once when the plan chose none
         if (p.pf_seq && p.pf_tiles) prefill_tiles_kernel<false><<<device_cus() * 4, 64 * PF_NSP, 0, stream>>>(p);
         const int rows = max_query_len * p.G;
-        const int tiles = (rows + PF_ROWS - 1) / PF_ROWS;
+        const int tiles = (rows + pl.pf_rows - 1) / pl.pf_rows;
         const dim3 grid = p.pf_seq ? dim3(pl.pf_grid_items * num_kv_heads) : dim3(tiles * num_kv_heads, num_seqs);
-        attn_prefill_kernel<QDT, ODT, false, false><<<grid, 64 * PF_WAVES, 0, stream>>>(p);
+        if (pl.pf_rows == PF_ROWS) attn_prefill_kernel<QDT, ODT, false, false><<<grid, 64 * PF_WAVES, 0, stream>>>(p);
+        else attn_prefill_kernel<QDT, ODT, false, false, 2><<<grid, 64 * PF_WAVES, 0, stream>>>(p);
         if (p.pf_seq && pl.pf_split_max)  // returns at once when the plan split nothing
             attn_prefill_combine_kernel<ODT><<<device_cus() * GFA_PFC_WGS_PER_CU, 256, 0, stream>>>(p);
     }
@@ -2411,7 +2571,7 @@ extern "C" int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tok
     const int64_t v[] = {(int64_t)(pl.bytes + pl.img_bytes), pl.ndc, pl.dec_rows_max, pl.need_prefill ? 1 : 0,
                          pl.pf_items_max, pl.pf_grid_items, pl.pf_split_max, pl.pf_slots_max,
                          pl.pf_items_max ? (int64_t)pl.off_items : -1, device_cus(), (int64_t)pl.bytes,
-                         (int64_t)pl.img_bytes};
+                         (int64_t)pl.img_bytes, pl.need_prefill ? pl.pf_rows : 0};
     const int n = (int)(sizeof(v) / sizeof(v[0]));
     for (int i = 0; i < n && i < info_len; ++i) info[i] = v[i];
     return n;
@@ -2554,6 +2714,7 @@ hipError_t paged_attention_impl(
     p.o_hs = out_head_stride;
     char *ws = static_cast<char *>(workspace);
     p.num_seqs = num_seqs;
+    p.pf_rows = pl.pf_rows;
     p.pf_items_max = pl.pf_items_max;
     p.pf_grid_items = pl.pf_grid_items;
     p.pf_ncu = device_cus();
@@ -2576,7 +2737,7 @@ hipError_t paged_attention_impl(
     // would decline them, and the pre-pass launch is skipped.
     p.pf_tbase = pl.pf_items_max ? reinterpret_cast<int *>(ws + pl.off_tbase) : nullptr;
     const size_t img_room = workspace_bytes > pl.bytes ? workspace_bytes - pl.bytes : 0;
-    const bool img_reuse = ((int64_t)max_query_len * G + PF_ROWS - 1) / PF_ROWS >= PF_IMG_REUSE;
+    const bool img_reuse = pl.pf_rows == PF_ROWS && ((int64_t)max_query_len * G + PF_ROWS - 1) / PF_ROWS >= PF_IMG_REUSE;
     p.pf_tiles = (pl.pf_items_max && img_reuse && img_room >= (size_t)PF_IMG_BYTES)
                      ? reinterpret_cast<uint8_t *>(ws + pl.bytes)
                      : nullptr;
@@ -2740,6 +2901,7 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_tiled(
     p.o_ts = out_token_stride;
     p.o_hs = out_head_stride;
     p.num_seqs = num_seqs;
+    p.pf_rows = PF_ROWS;
     p.dec_rows_max = 0;  // every sequence through the tiled kernel
     const int rows = max(max_query_len, 1) * p.G;
     const dim3 grid(((rows + PF_ROWS - 1) / PF_ROWS) * num_kv_heads, num_seqs);

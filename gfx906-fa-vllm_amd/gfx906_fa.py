@@ -78,6 +78,8 @@ def _load():
         "gfx906_fa_amd_paged_attention_workspace_bound": (SZ, [I, I64, I, I, I]),
         "gfx906_fa_amd_paged_attention_plan_info": (I, [I, I, I, I, I, I, I, P, I]),
         "gfx906_fa_amd_device_cus": (I, []),
+        "gfx906_fa_amd_stream_read_words": (I, []),
+        "gfx906_fa_amd_stream_read": (I, [P, I64, P, I, P]),
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
         "gfx906_fa_amd_paged_attention_kv_write": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
@@ -386,7 +388,8 @@ def workspace_bound(max_num_seqs: int, max_num_tokens: int, num_heads: int, num_
 
 
 PLAN_FIELDS = ("bytes", "decode_classes", "dec_rows_max", "prefill", "pf_items_max", "pf_grid_items",
-               "pf_split_max", "pf_slots_max", "pf_header_offset", "cus", "img_offset", "img_bytes")
+               "pf_split_max", "pf_slots_max", "pf_header_offset", "cus", "img_offset", "img_bytes",
+               "pf_rows")
 
 
 def plan_info(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int, max_query_len: int,
@@ -399,7 +402,8 @@ def plan_info(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int,
     workspace_size) is ``img_offset``, the regions every call needs, plus
     ``img_bytes`` of room for those images; a smaller workspace of at least
     ``img_offset`` bytes runs the same call with the prefill workgroups
-    dequantizing every tile themselves."""
+    dequantizing every tile themselves.  ``pf_rows``: query rows per prefill
+    row tile (256, or 128 for key-interleaved tiles; 0 without prefill)."""
     buf = (ctypes.c_int64 * len(PLAN_FIELDS))()
     n = _load().gfx906_fa_amd_paged_attention_plan_info(num_seqs, num_tokens, num_heads, num_kv_heads,
                                                          head_size, max_query_len, max_seq_len, buf,
@@ -411,6 +415,21 @@ def plan_info(num_seqs: int, num_tokens: int, num_heads: int, num_kv_heads: int,
 def device_cus() -> int:
     """CUs of the current device the plans target (256 without a device)."""
     return int(_load().gfx906_fa_amd_device_cus())
+
+
+def stream_read(src: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Reads every byte of the contiguous device tensor ``src`` once (a
+    read-only streaming ceiling for measurements) and returns the per-wave
+    XOR words.  Not part of the reference interface."""
+    _check(src.is_cuda and src.is_contiguous(), "stream_read: src must be a contiguous CUDA/HIP tensor")
+    nw = int(_load().gfx906_fa_amd_stream_read_words())
+    if out is None:
+        out = torch.empty(nw, dtype=torch.int32, device=src.device)
+    _check(out.is_cuda and out.numel() >= nw and out.element_size() == 4, "stream_read: out too small")
+    err = _load().gfx906_fa_amd_stream_read(src.data_ptr(), src.numel() * src.element_size(), out.data_ptr(),
+                                             out.numel(), _stream(src.device))
+    _check(err == 0, f"stream_read failed ({err})")
+    return out
 
 
 def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,

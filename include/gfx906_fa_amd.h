@@ -234,8 +234,11 @@ size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs, int64_t m
  *     int32 1 if the tiles were dequantized once as images, int32 image
  *     tiles per kv-head; written by the call; -1 without a work list), [9]
  *     CUs planned for, [10] the workspace bytes every call needs (the image
- *     room starts there), [11] the image room (info[0] = [10] + [11]).
- *     Returns the number of entries (12; at most info_len are written), or
+ *     room starts there), [11] the image room (info[0] = [10] + [11]),
+ *     [12] query rows per prefill row tile (256, or 128 for the
+ *     key-interleaved tiles chosen when the longest prefill sequence has at
+ *     most 128 rows per kv-head; 0 without a prefill launch).
+ *     Returns the number of entries (13; at most info_len are written), or
  *     -1 for an invalid shape.  No reference counterpart. */
 int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tokens, int num_heads,
                                             int num_kv_heads, int head_size, int max_query_len,
@@ -357,6 +360,15 @@ hipError_t gfx906_fa_amd_paged_attention_tiled(
     int num_seqs, int num_tokens, int num_heads, int num_kv_heads, int head_size,
     int block_size, int max_query_len, float scale, float *out, int64_t out_token_stride,
     int64_t out_head_stride, hipStream_t stream);
+
+/* Measurement helper: streams `bytes` (a multiple of 16) from the 16-byte
+ * aligned device buffer `src` with non-temporal 16-byte loads and writes one
+ * XOR word per wave to `out` (at least gfx906_fa_amd_stream_read_words()
+ * words).  Its rate is the read-only streaming ceiling the read-dominated
+ * attention passes are compared with.  No reference counterpart. */
+int gfx906_fa_amd_stream_read_words(void);
+hipError_t gfx906_fa_amd_stream_read(const void *src, int64_t bytes, uint32_t *out, int out_words,
+                                     hipStream_t stream);
 
 #ifdef __cplusplus
 }

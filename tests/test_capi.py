@@ -164,6 +164,16 @@ def test_plan_info():
     assert (s36["decode_classes"], s36["dec_rows_max"], s36["prefill"]) == (1, 64, 0)
     smix = gfx906_fa.plan_info(4, 18, 6, 1, 6, 3000)
     assert (smix["decode_classes"], smix["dec_rows_max"], smix["prefill"]) == (2, 64, 0)
+    # prefill tile rows: 128-row key-interleaved tiles up to 128 rows per
+    # kv-head (the longest sequence's), 256-row tiles above
+    assert d["pf_rows"] == 0 and m["pf_rows"] == 256
+    for q, G, want in ((11, 6, 128), (12, 6, 128), (16, 8, 128), (128, 1, 128), (129, 1, 256), (32, 6, 256),
+                       (51, 5, 256), (50, 6, 256), (48, 8, 256), (32768, 6, 256)):
+        info = gfx906_fa.plan_info(1, q, 8 * G, 8, q, 65536)
+        assert info["pf_rows"] == want, (q, G, info["pf_rows"])
+    assert g40["pf_rows"] == 128                              # 120 rows beside decode rows
+    pc = gfx906_fa.plan_info(33, 12 + 32, 48, 8, 12, 32768)   # 32 decodes + a 12-token chunk
+    assert (pc["decode_classes"], pc["dec_rows_max"], pc["pf_rows"]) == (2, 64, 128)
     with pytest.raises(RuntimeError):
         gfx906_fa.plan_info(1, 1, 6, 4, 1, 1)             # heads not divisible
 

@@ -1,6 +1,6 @@
 """GPU: prefill row tiles split over their keys.
 
-A launch whose prefill row tiles (256 packed rows of one sequence and kv head)
+A launch whose prefill row tiles (256 or 128 packed rows of one sequence and kv head)
 are few and long - a prefix-cached chunk of tens to hundreds of tokens after a
 long context, or a batch of such - has its row tiles cut into key ranges that
 separate workgroups run; a combine kernel merges their partial (m, l, O).  The
@@ -73,8 +73,9 @@ def test_split_prefill_matches_oracle(case):
     out = W.attention(b, out_dtype=torch.float32, workspace=ws)
     torch.cuda.synchronize()
     items, nsplit = _split_header(ws, b)
-    dec_max = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, Hq, Hkv, b.max_query_len, b.max_seq_len)["dec_rows_max"]
-    tiles = sum(-(-q * (Hq // Hkv) // 256) for q in qls if q * (Hq // Hkv) > dec_max)
+    info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, Hq, Hkv, b.max_query_len, b.max_seq_len)
+    dec_max, prow = info["dec_rows_max"], info["pf_rows"]
+    tiles = sum(-(-q * (Hq // Hkv) // prow) for q in qls if q * (Hq // Hkv) > dec_max)
     # the plan split something: pieces beyond the row tiles, split row tiles listed
     assert nsplit > 0 and items > tiles, (items, nsplit, tiles)
     if name.startswith("many_tiles"):
