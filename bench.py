@@ -17,9 +17,11 @@ Also reported on the same JSON line:
                   its average duration from HIP events on the launch stream,
                   against 8 TB/s; ``traffic`` from the committed rocprofv3
                   FETCH_SIZE/WRITE_SIZE measurement when present;
-                  ``copy_ceiling_gbs`` a plain 1 GiB device copy (read + write
-                  bytes / time) on the same GPU, and ``frac_of_copy`` the
-                  attention rate against it.
+                  ``read_ceiling_gbs`` the library's read-only streaming
+                  kernel over 2 GiB on the same GPU and
+                  ``frac_of_read_ceiling`` the attention rate against it;
+                  ``copy_gbs`` a plain 1 GiB device copy (read + write bytes /
+                  time), for comparison.
   prefill       - cfg3 (32K causal prefill, bf16, 48/8): attention TFLOP/s
                   (4*D*Hq*sum of visible keys) vs 2.5 PFLOP/s dense fp16/bf16
                   MFMA peak, ``mfma_busy`` (the MFMA-busy fraction of the
@@ -27,6 +29,11 @@ Also reported on the same JSON line:
                   summary), the K/V quantize-write GB/s, and the fused
                   rotary + K/V write GB/s (vs 8 TB/s) over the same tokens,
                   for the bf16 model and again for an fp16 one.
+  configs       - the benchmark definition's other configurations, one timed
+                  pass set each (the rows --workload prints in full): cfg4
+                  (fraction of the summed MFMA + HBM roofline time, with its
+                  prefill and decode parts timed alone), cfg5 at 6/1 and at
+                  48/8, and the 6-token n-gram verify step at 6/1 (GB/s).
   next_rows     - graph capture: the cfg2 step and a 32 x 32-token decode
                   batch per call, eager vs replayed from a HIP graph; the
                   output epilogue: the reference's fp32 BSHD -> BHSD ->
@@ -117,6 +124,15 @@ def timed(fn, steps: int, warmup: int):
     e.record(stream)
     torch.cuda.synchronize()
     return s.elapsed_time(e) / steps
+
+
+def timed_warm(fn, steps: int, warmup: int, min_warm_ms: float = 50.0):
+    """timed() with at least ``min_warm_ms`` of device work as warm-up:
+    back-to-back passes run up to 7 % slower over the first ~10-20 ms after
+    set-up (and after a new batch was written), so a handful of warm-up
+    passes is not enough for short ones."""
+    est = timed(fn, 1, 1)
+    return timed(fn, steps, max(warmup, int(min_warm_ms / max(est, 1e-3)) + 1))
 
 
 def graph_timed(fn, calls: int = 20, replays: int = 10):
@@ -267,17 +283,18 @@ def _attn_fn(b, out, ws):
     return f
 
 
-def other_workload(args, dev) -> dict:
+def workload_result(wl: str, dev, steps: int, warmup: int) -> dict:
     """One attention pass of cfg3 / cfg4 / cfg5 (inputs resident in HBM),
-    timed with HIP events on the launch stream."""
+    timed with HIP events on the launch stream: the full JSON line of
+    ``--workload wl``."""
     import torch
 
     import gfx906_fa
     import gfx906_fa_workloads as W
 
-    name = {"cfg5-48": "cfg5", "cfg5-k6": "cfg5k6"}.get(args.workload, args.workload)
+    name = {"cfg5-48": "cfg5", "cfg5-k6": "cfg5k6"}.get(wl, wl)
     verify = name in ("cfg5", "cfg5k6")
-    heads = (48, 8) if args.workload == "cfg5-48" else None
+    heads = (48, 8) if wl == "cfg5-48" else None
     b = W.build_cfg(name, device=dev, heads=heads)
     odt = torch.bfloat16 if b.dtype == "bf16" else torch.float16
 
@@ -288,16 +305,16 @@ def other_workload(args, dev) -> dict:
         return gfx906_fa.new_workspace(gfx906_fa.workspace_size(
             bb.num_seqs, bb.num_tokens, bb.Hq, bb.Hkv, bb.max_query_len, bb.max_seq_len), dev)
 
-    steps = args.steps if verify else max(3, min(10, args.steps // 5))
-    # warm-up: the given steps, at least ~20 ms of work for the short passes
-    ms = timed(_attn_fn(b, new_out(b), new_ws(b)), steps, max(2, args.warmup if verify else 2))
+    steps = steps if verify else max(3, min(10, steps // 5))
+    # warm-up: the given steps, and at least ~50 ms of device work
+    ms = timed_warm(_attn_fn(b, new_out(b), new_ws(b)), steps, max(2, warmup if verify else 2))
     fl, hb = b.flops(), b.hbm_bytes(out_bytes_per_elem=2)
     gbs, tfs = hb / (ms * 1e-3) / 1e9, fl / (ms * 1e-3) / 1e12
     res = {
         "metric": "Q8 paged decode HBM GB/s (% of peak); causal prefill attn TFLOP/s @32K",
         "n_gpus": 1, "steps": steps, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": b.dtype, "data": "synthetic",
-        "config": {"workload": f"{args.workload}: {W.CONFIGS[name]}", "num_seqs": b.num_seqs,
+        "config": {"workload": f"{wl}: {W.CONFIGS[name]}", "num_seqs": b.num_seqs,
                    "num_tokens": b.num_tokens, "heads": f"{b.Hq}/{b.Hkv}", "total_context": int(b.seq_lens.sum()),
                    "algorithmic_bytes": hb, "flop": fl, "parallelism": "single GPU"},
     }
@@ -315,8 +332,8 @@ def other_workload(args, dev) -> dict:
     else:  # cfg4: both bounds; the parts timed as batches of their own
         npf = int((b.q_lens > 1).sum())
         pf, dc = W.sub_batch(b, 0, npf), W.sub_batch(b, npf, b.num_seqs)
-        ms_pf = timed(_attn_fn(pf, new_out(pf), new_ws(pf)), steps, 2)
-        ms_dc = timed(_attn_fn(dc, new_out(dc), new_ws(dc)), max(steps, 20), 40)
+        ms_pf = timed_warm(_attn_fn(pf, new_out(pf), new_ws(pf)), steps, 2)
+        ms_dc = timed_warm(_attn_fn(dc, new_out(dc), new_ws(dc)), max(steps, 20), 40)
         t_roof = pf.flops() / (MFMA_PEAK_TFLOPS * 1e12) + dc.hbm_bytes(2) / (HBM_PEAK_GBS * 1e9)
         res.update({"value": round(t_roof / (ms * 1e-3), 4), "unit": "fraction of the summed roofline time"})
         res["roofline"] = {"bound": "mfma+hbm", "kernel": "attn_prefill_kernel+attn_decode_kernel",
@@ -330,7 +347,29 @@ def other_workload(args, dev) -> dict:
                             "gbs": round(dc.hbm_bytes(2) / (ms_dc * 1e-3) / 1e9, 1),
                             "frac_of_hbm_peak": round(dc.hbm_bytes(2) / (ms_dc * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         }
+    del b
+    torch.cuda.empty_cache()
     return res
+
+
+def config_rows(dev, steps: int, warmup: int) -> dict:
+    """The benchmark definition's other configurations, one timed pass set
+    each, for the default line: cfg4 (mixed chunked prefill + decode: the
+    fraction of the summed MFMA + HBM roofline time), cfg5 at 6/1 (5 verify
+    tokens, the tensor-parallel shard) and 48/8, and the reference's n-gram
+    verify step (6 tokens, k = 5) at 6/1 (HBM GB/s against 8 TB/s)."""
+    rows = {}
+    for wl in ("cfg4", "cfg5", "cfg5-48", "cfg5-k6"):
+        r = workload_result(wl, dev, steps, warmup)
+        e = {"workload": r["config"]["workload"], "heads": r["config"]["heads"], "passes": r["steps"],
+             "ms": r["ms_per_step"], "value": r["value"], "unit": r["unit"], "frac": r["roofline"]["frac"]}
+        if "parts" in r:
+            e["summed_roofline_ms"] = r["roofline"]["achieved"]
+            e["parts"] = r["parts"]
+        else:
+            e["bytes"] = r["config"]["algorithmic_bytes"]
+        rows[wl] = e
+    return rows
 
 
 def main() -> int:
@@ -343,6 +382,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the cfg4 / cfg5 rows of the default line")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (rocprof counter calibration)")
@@ -362,7 +402,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.workload != "cfg2":
-        print(json.dumps(other_workload(args, dev)), flush=True)
+        print(json.dumps(workload_result(args.workload, dev, args.steps, args.warmup)), flush=True)
         return 0
 
     # ---------------- cfg2 decode -----------------------------------------
@@ -393,24 +433,30 @@ def main() -> int:
     # Pre-warm.  Back-to-back passes run up to 7 % slower over the first
     # ~10-20 ms of device work after set-up (successive 60-step loops of the
     # cfg2 step measured 115, 110 and 108 us), and the driver's --warmup is a
-    # handful of steps.  So the copy-ceiling measurement (a plain 1 GiB
-    # device copy, read + write bytes over its time: the streaming ceiling of
-    # this part) and PREWARM_PASSES attention passes run first; their device
-    # time is reported as ``prewarm_ms``, apart from the --warmup steps.
+    # handful of steps.  So the ceiling measurements and PREWARM_PASSES
+    # attention passes run first; their device time is reported as
+    # ``prewarm_ms``, apart from the --warmup steps.  The ceilings: the
+    # library's read-only streaming kernel over 2 GiB (the bound for a pass
+    # that reads ~1000x what it writes), and a plain 1 GiB device copy (read
+    # + write bytes over its time, reported for comparison).
     stream = torch.cuda.current_stream()
     csrc = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     cdst = torch.empty_like(csrc)
+    rsrc = torch.ones(1 << 29, dtype=torch.float32, device=dev)
+    rwords = torch.empty(gfx906_fa.lib().gfx906_fa_amd_stream_read_words(), dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
     pw0, pw1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     pw0.record(stream)
     ms_copy = timed(lambda: cdst.copy_(csrc), 20, 5)
     copy_gbs = 2 * csrc.numel() * 4 / (ms_copy * 1e-3) / 1e9
+    ms_read = timed(lambda: gfx906_fa.stream_read(rsrc, rwords), 20, 5)
+    read_gbs = rsrc.numel() * 4 / (ms_read * 1e-3) / 1e9
     for _ in range(PREWARM_PASSES):
         attn()
     pw1.record(stream)
     torch.cuda.synchronize()
     prewarm_ms = pw0.elapsed_time(pw1)
-    del csrc, cdst
+    del csrc, cdst, rsrc, rwords
 
     # the headline: exactly --steps steps after --warmup steps
     ms_step = timed(step, args.steps, args.warmup)
@@ -448,12 +494,13 @@ def main() -> int:
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic, "algorithmic_bytes": attn_bytes, "avg_us": round(ms_attn * 1e3, 2),
-            "copy_ceiling_gbs": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4),
-            "timed_passes": attn_calls,
+            "read_ceiling_gbs": round(read_gbs, 1), "frac_of_read_ceiling": round(achieved / read_gbs, 4),
+            "copy_gbs": round(copy_gbs, 1), "timed_passes": attn_calls,
         },
         "prewarm_ms": round(prewarm_ms, 2),
-        "prewarm": f"before timing: a 1 GiB device copy x 25 and {PREWARM_PASSES} attention passes "
-                   f"({prewarm_ms:.1f} ms of device work), then the {args.warmup} --warmup steps",
+        "prewarm": f"before timing: a 1 GiB device copy x 25, a 2 GiB read-only stream x 25 and "
+                   f"{PREWARM_PASSES} attention passes ({prewarm_ms:.1f} ms of device work), then the "
+                   f"{args.warmup} --warmup steps",
     }
 
     # ---------------- the rows after the hot path -------------------------
@@ -541,6 +588,10 @@ def main() -> int:
             del pk_aos, pv_aos, q3
         del p, pout
         torch.cuda.empty_cache()
+
+    # ---------------- the other configurations ---------------------------
+    if not args.no_configs and not args.calib_copy_mib:
+        res["configs"] = config_rows(dev, args.steps, args.warmup)
 
     if graph is not None:
         res["next_rows"] = {"graph_replay": graph,

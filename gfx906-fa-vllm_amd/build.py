@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_NAME = "libgfx906_fa_amd.so"
-SOURCES = ["q8_quant.hip", "q8_rope.hip", "q8_gather.hip", "q8_pack.hip", "paged_attn.hip"]
+SOURCES = ["q8_quant.hip", "q8_rope.hip", "q8_gather.hip", "q8_pack.hip", "paged_attn.hip", "hbm_probe.hip"]
 ARCH = os.environ.get("GFX906_FA_AMD_ARCH", "gfx950")
 
 

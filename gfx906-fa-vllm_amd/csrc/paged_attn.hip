@@ -2612,6 +2612,23 @@ hipError_t scratch_address(void **out) {
     return hipSuccess;
 }
 
+}  // namespace
+
+extern "C" hipError_t gfx906_fa_amd_noalloc_scratch_copy(void *dst, size_t offset, size_t bytes, hipStream_t stream) {
+    if (dst == nullptr || offset > GFX906_FA_AMD_SCRATCH_BYTES || bytes > GFX906_FA_AMD_SCRATCH_BYTES - offset) {
+        fprintf(stderr, "[gfx906_fa_amd] noalloc_scratch_copy: range past the %zu-byte scratch\n",
+                (size_t)GFX906_FA_AMD_SCRATCH_BYTES);
+        return hipErrorInvalidValue;
+    }
+    if (bytes == 0) return hipSuccess;
+    void *a = nullptr;
+    const hipError_t e = scratch_address(&a);
+    if (e != hipSuccess) return e;
+    return hipMemcpyAsync(dst, static_cast<char *>(a) + offset, bytes, hipMemcpyDeviceToDevice, stream);
+}
+
+namespace {
+
 // The step's new K/V rows for the fused cache write (element strides).
 struct NewKV {
     const void *key, *value;

@@ -80,6 +80,9 @@ def _load():
         "gfx906_fa_amd_device_cus": (I, []),
         "gfx906_fa_amd_stream_read_words": (I, []),
         "gfx906_fa_amd_stream_read": (I, [P, I64, P, I, P]),
+        "gfx906_fa_amd_noalloc_scratch_copy": (I, [P, SZ, SZ, P]),
+        "gfx906_fa_amd_paged_attention_noalloc": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
+                                                      I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P]),
         "gfx906_fa_amd_paged_attention": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,
                                               I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ, P]),
         "gfx906_fa_amd_paged_attention_kv_write": (I, [P, I, I64, I64, P, P, I64, I64, P, I64, P, P, P,

@@ -288,6 +288,14 @@ hipError_t gfx906_fa_amd_paged_attention_noalloc(
     void *out, int out_dtype, int64_t out_token_stride, int64_t out_head_stride,
     hipStream_t stream);
 
+/* (5n-copy) Diagnostics for (5n): copies `bytes` of the current device's
+ *      scratch, from byte `offset`, to the device buffer `dst` (an ordinary
+ *      stream-ordered copy).  With plan_info()'s work-list header offset it
+ *      shows which prefill path the last (5n) call took.  Offsets past the
+ *      scratch are refused (hipErrorInvalidValue).  No reference
+ *      counterpart. */
+hipError_t gfx906_fa_amd_noalloc_scratch_copy(void *dst, size_t offset, size_t bytes, hipStream_t stream);
+
 /* (5b) (4) followed by (5) in one call: key / value [num_tokens, Hkv, D] (the
  *      query dtype, element strides) are quantized to Q8_0 and written at
  *      slot_mapping[t] (< 0 = skip) before attention reads the cache.  When

@@ -82,6 +82,23 @@ def test_validation_errors_without_gpu():
                                                    None, 1, 1, 1, 8, 1, 128, 16, 1, 16, 0.1, None, 1, 0,
                                                    0, None, 0, None, None, 1, 0, 0, 0, 0, None, None)
     assert err == 1
+    # streaming-read helper: a byte count that is not a multiple of 16, or too
+    # few output words, is refused before any launch; zero bytes is a no-op
+    nw = L.gfx906_fa_amd_stream_read_words()
+    assert nw > 0
+    assert L.gfx906_fa_amd_stream_read(None, 0, None, 0, None) == 0
+    assert L.gfx906_fa_amd_stream_read(None, 24, None, nw, None) == 1
+    assert L.gfx906_fa_amd_stream_read(None, 32, None, nw - 1, None) == 1
+    # allocation-free attention: a batch whose plan exceeds the library's
+    # scratch is refused on the host, before the scratch is looked up or any
+    # work is enqueued (no device needed)
+    f = L.gfx906_fa_amd_paged_attention_noalloc
+    big_b = 40_000_000  # per-sequence prefix sums alone exceed 64 MiB
+    assert f(None, 1, 0, 0, None, None, 0, 0, None, 0, None, None, None, 1, big_b, big_b, 48, 8, 128,
+             16, 1, 16, 0.1, None, 1, 0, 0, None) == 1
+    # the scratch copy helper refuses ranges past the scratch
+    assert L.gfx906_fa_amd_noalloc_scratch_copy(None, 0, 16, None) == 1
+    assert L.gfx906_fa_amd_noalloc_scratch_copy(ctypes.c_void_p(16), 64 << 20, 16, None) == 1
 
 
 def test_workspace_size_plan():
