@@ -2308,11 +2308,13 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Splits the softmax scale c between Q and K^ for the prefill kernel:
 // Q * 2^-e (exact) and K^ * (c * 2^e), with e chosen so that c * 2^e is in
-// [1, 2): K^ keeps about the magnitude of the dequantized keys.
+// [0.5, 1): K^ = fp16(q * d_k * kmul) stays at or below the dequantized key
+// q * d_k, so it is finite wherever the decode kernel's fp16(q * d_k) is
+// (a kmul up to 2 would overflow keys above 65504 / kmul, 32.8K at worst).
 void set_prefill_scale(AttnParams &p) {
     int e = 0;
     (void)frexpf(p.scale_log2e, &e);  // c = m * 2^e, m in [0.5, 1)
-    e = max(-60, min(60, 1 - e));
+    e = max(-60, min(60, -e));
     p.pf_qmul = ldexpf(1.0f, -e);
     p.pf_kmul = ldexpf(p.scale_log2e, e);
 }
@@ -2465,7 +2467,8 @@ Plan make_plan(int num_seqs, int num_tokens, int num_heads, int num_kv_heads, in
 // 32-row class), and a prefill work list sized for max_num_tokens.
 // plan_finish's regions are monotone in all of these, and the decode
 // regions a call lays out sum to at most those laid out here.
-Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num_kv_heads, bool allow_split) {
+Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num_kv_heads, bool allow_split,
+                int64_t max_seq_len = -1) {
     Plan pl{};
     const int G = num_heads / num_kv_heads;
     pl.ndc = 0;
@@ -2474,7 +2477,7 @@ Plan bound_plan(int max_num_seqs, int64_t max_num_tokens, int num_heads, int num
     if (G <= DEC_CHUNK_ROWS) plan_add_class(pl, 2, pl.ndc ? pl.dc[pl.ndc - 1].rows_hi : 0, DEC_CHUNK_ROWS);
     pl.need_prefill = true;
     pl.pf_rows = PF_ROWS / 2;  // the smaller tile: the most row tiles
-    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, -1, max_num_tokens);
+    plan_finish(pl, max_num_seqs, max_num_tokens, G, num_kv_heads, true, allow_split, max_seq_len, max_num_tokens);
     return pl;
 }
 
@@ -2557,6 +2560,21 @@ extern "C" size_t gfx906_fa_amd_paged_attention_workspace_bound(int max_num_seqs
         return 0;
     const Plan pl = bound_plan(max_num_seqs, max_num_tokens, num_heads, num_kv_heads, true);
     return pl.bytes + pl.img_bytes;
+}
+
+extern "C" int gfx906_fa_amd_paged_attention_workspace_bound_info(int max_num_seqs, int64_t max_num_tokens,
+                                                                  int num_heads, int num_kv_heads, int head_size,
+                                                                  int64_t max_seq_len, int64_t *info, int info_len) {
+    (void)head_size;
+    if (info == nullptr || max_num_seqs <= 0 || max_num_tokens < 0 || num_kv_heads <= 0 || num_heads <= 0 ||
+        num_heads % num_kv_heads)
+        return -1;
+    const Plan pl = bound_plan(max_num_seqs, max_num_tokens, num_heads, num_kv_heads, true,
+                               max_seq_len > 0 ? max_seq_len : -1);
+    const int64_t v[] = {(int64_t)pl.bytes, (int64_t)pl.img_bytes};
+    const int n = (int)(sizeof(v) / sizeof(v[0]));
+    for (int i = 0; i < n && i < info_len; ++i) info[i] = v[i];
+    return n;
 }
 
 extern "C" int gfx906_fa_amd_device_cus(void) { return device_cus(); }

@@ -77,6 +77,7 @@ def _load():
         "gfx906_fa_amd_paged_attention_workspace_size": (SZ, [I, I, I, I, I, I, I]),
         "gfx906_fa_amd_paged_attention_workspace_bound": (SZ, [I, I64, I, I, I]),
         "gfx906_fa_amd_paged_attention_plan_info": (I, [I, I, I, I, I, I, I, P, I]),
+        "gfx906_fa_amd_paged_attention_workspace_bound_info": (I, [I, I64, I, I, I, I64, P, I]),
         "gfx906_fa_amd_device_cus": (I, []),
         "gfx906_fa_amd_stream_read_words": (I, []),
         "gfx906_fa_amd_stream_read": (I, [P, I64, P, I, P]),
@@ -388,6 +389,21 @@ def workspace_bound(max_num_seqs: int, max_num_tokens: int, num_heads: int, num_
     query lengths and mix (decode, verify, prefill)."""
     return int(_load().gfx906_fa_amd_paged_attention_workspace_bound(
         int(max_num_seqs), int(max_num_tokens), num_heads, num_kv_heads, head_size))
+
+
+def workspace_bound_info(max_num_seqs: int, max_num_tokens: int, num_heads: int, num_kv_heads: int,
+                         max_seq_len: int = -1, head_size: int = 128) -> dict:
+    """The workspace bound in its two parts: ``regions``, the bytes every
+    call within the limits needs (its plan_info ``img_offset`` is at most
+    this), and ``img_bytes``, the room for prefill tile images of contexts up
+    to max_seq_len keys (-1: any context; the library's 1 GiB cap).  The
+    image room is optional: with ``regions`` bytes every such call runs,
+    dequantizing its own prefill tiles where images do not fit."""
+    buf = (ctypes.c_int64 * 2)()
+    n = _load().gfx906_fa_amd_paged_attention_workspace_bound_info(
+        int(max_num_seqs), int(max_num_tokens), num_heads, num_kv_heads, head_size, int(max_seq_len), buf, 2)
+    _check(n == 2, f"workspace_bound_info: invalid shape (returned {n})")
+    return {"regions": int(buf[0]), "img_bytes": int(buf[1])}
 
 
 PLAN_FIELDS = ("bytes", "decode_classes", "dec_rows_max", "prefill", "pf_items_max", "pf_grid_items",
@@ -798,8 +814,10 @@ def _register_torch_ops() -> None:
         """The backend's step: attention into ``out`` (the model dtype), with
         the step's K/V written to the cache first when new_key / new_value /
         slot_mapping are given (the caches are in-place arguments for that)."""
-        need = workspace_size(seq_lens.shape[0], query.shape[0], query.shape[1], key_cache.shape[1],
-                              max_query_len, max_seq_len)
+        # the regions every call needs; the tile-image room past them is
+        # optional (without it the prefill workgroups dequantize their tiles)
+        need = plan_info(seq_lens.shape[0], query.shape[0], query.shape[1], key_cache.shape[1],
+                         max_query_len, max_seq_len, query.shape[2])["img_offset"]
         _check(workspace is None or workspace.numel() * workspace.element_size() >= need,
                f"paged_attention_out: workspace needs {need} bytes")
         paged_attention(query, key_cache, value_cache, block_table, seq_lens, query_start_loc, max_query_len,

@@ -22,6 +22,7 @@ What differs, by design:
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 from typing import ClassVar
 
@@ -69,13 +70,45 @@ class Gfx906FAMetadata:
     common_prefix_len: int = 0
 
 
-def workspace_upper_bound(max_num_seqs: int, max_num_tokens: int, heads) -> int:
+def workspace_upper_bound(max_num_seqs: int, max_num_tokens: int, heads, max_seq_len: int = -1,
+                          image_room: int | None = None) -> int:
     """Attention workspace that covers every batch of up to max_num_seqs
     sequences and max_num_tokens query tokens - any query lengths, any mix of
     decode, speculative-verify and prefill sequences, any context - for each
-    layer shape (num_heads, num_kv_heads) in ``heads``."""
-    return max((gfx906_fa.workspace_bound(max_num_seqs, max_num_tokens, hq, hkv) for hq, hkv in heads),
-               default=0)
+    layer shape (num_heads, num_kv_heads) in ``heads``: the regions every
+    such call needs plus the prefill tile-image room for contexts up to
+    max_seq_len (-1: any), capped at ``image_room`` bytes when given (the
+    room is optional: prefill workgroups dequantize their own tiles where
+    images do not fit)."""
+    best = 0
+    for hq, hkv in heads:
+        i = gfx906_fa.workspace_bound_info(max_num_seqs, max_num_tokens, hq, hkv, max_seq_len)
+        img = i["img_bytes"] if image_room is None else min(i["img_bytes"], max(int(image_room), 0))
+        best = max(best, i["regions"] + img)
+    return best
+
+
+def image_room_bytes() -> int:
+    """The tile-image room the backend reserves at most: GFX906_FA_IMAGE_ROOM_MB
+    (default 256 MiB, enough for the images of a 57K-token prompt at 8
+    kv-heads; 0 turns prefill tile images off)."""
+    try:
+        mb = int(os.environ.get("GFX906_FA_IMAGE_ROOM_MB", "256"))
+    except ValueError:
+        mb = 256
+    return max(mb, 0) << 20
+
+
+def _scheduler_limits(vllm_config) -> tuple[int, int, int] | None:
+    """(max_num_seqs, max_num_batched_tokens, max_model_len or -1) of a vLLM
+    config, or None where the scheduler limits are not set."""
+    sched = getattr(vllm_config, "scheduler_config", None)
+    max_seqs = getattr(sched, "max_num_seqs", None)
+    max_tokens = getattr(sched, "max_num_batched_tokens", None)
+    if not (isinstance(max_seqs, int) and max_seqs > 0 and isinstance(max_tokens, int) and max_tokens > 0):
+        return None
+    mml = getattr(getattr(vllm_config, "model_config", None), "max_model_len", None)
+    return max_seqs, max_tokens, mml if isinstance(mml, int) and mml > 0 else -1
 
 
 class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
@@ -92,10 +125,12 @@ class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
         # Reserve the shared workspace before any capture, so forward() never
         # allocates inside a graph: the bound over the scheduler's batch
         # limits for every layer shape seen (the Impls are built with the
-        # model, before the builders).
-        sched = getattr(vllm_config, "scheduler_config", None)
-        max_seqs = getattr(sched, "max_num_seqs", None)
-        max_tokens = getattr(sched, "max_num_batched_tokens", None)
+        # model, before the builders).  The profiling forward has normally
+        # reserved it already (so vLLM's memory profile counts it); this
+        # covers layer shapes seen only now.
+        limits = _scheduler_limits(vllm_config)
+        if limits is not None:
+            Gfx906FAImpl._limits = limits
         heads = set(Gfx906FAImpl._layer_heads)
         hkv = getattr(kv_cache_spec, "num_kv_heads", None)
         model_config = getattr(vllm_config, "model_config", None)
@@ -104,13 +139,14 @@ class Gfx906FAMetadataBuilder(AttentionMetadataBuilder[Gfx906FAMetadata]):
                 heads.add((int(model_config.get_num_attention_heads(vllm_config.parallel_config)), hkv))
             except (AttributeError, TypeError, ValueError):
                 pass
-        if (isinstance(max_seqs, int) and max_seqs > 0 and isinstance(max_tokens, int) and max_tokens > 0
-                and heads and torch.device(device).type == "cuda"):
-            Gfx906FAImpl.reserve_workspace(workspace_upper_bound(max_seqs, max_tokens, heads),
-                                           torch.device(device))
+        if limits is not None and heads and torch.device(device).type == "cuda":
+            Gfx906FAImpl.reserve_workspace(Gfx906FAImpl.bound_bytes(heads, limits), torch.device(device))
 
     def build_for_cudagraph_capture(self, common_attn_metadata: CommonAttentionMetadata
                                     ) -> Gfx906FAMetadata:
+        # a graph captured from here keeps the workspace's raw address: from
+        # now on a replaced workspace must stay allocated
+        Gfx906FAImpl._captured = True
         return self.build(0, common_attn_metadata)
 
     def build(self, common_prefix_len: int, common_attn_metadata: CommonAttentionMetadata,
@@ -246,14 +282,18 @@ class Gfx906FAImpl(AttentionImpl):
     # shares its gather buffers the same way, lines 229-230).  Layers run in
     # order on one stream, so reuse is safe.
     _workspace: ClassVar[torch.Tensor | None] = None
-    # Workspaces replaced by a larger one.  A captured graph holds the raw
-    # address of the workspace it was captured with (the kernels receive
-    # pointers, so the graph keeps no reference to the tensor): a replaced
-    # workspace stays allocated for the life of the process, since later
-    # replays still write into it.
+    # Workspaces replaced by a larger one after a graph capture.  A captured
+    # graph holds the raw address of the workspace it was captured with (the
+    # kernels receive pointers, so the graph keeps no reference to the
+    # tensor): such a workspace stays allocated for the life of the process,
+    # since later replays still write into it.  Before any capture a replaced
+    # workspace is simply freed.
     _retired: ClassVar[list[torch.Tensor]] = []
+    _captured: ClassVar[bool] = False
     # (num_heads, num_kv_heads) of every layer built, for the workspace bound
     _layer_heads: ClassVar[set[tuple[int, int]]] = set()
+    # (max_num_seqs, max_num_batched_tokens, max_model_len) of the scheduler
+    _limits: ClassVar[tuple[int, int, int] | None] = None
 
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
                  alibi_slopes: list[float] | None, sliding_window: int | None,
@@ -286,6 +326,14 @@ class Gfx906FAImpl(AttentionImpl):
         self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
         self.num_queries_per_kv = num_heads // num_kv_heads
         Gfx906FAImpl._layer_heads.add((num_heads, num_kv_heads))
+        if Gfx906FAImpl._limits is None:
+            # the scheduler limits of the model being built (set by vLLM
+            # around model construction), for the profiling forward
+            try:
+                from vllm.config import get_current_vllm_config
+                Gfx906FAImpl._limits = _scheduler_limits(get_current_vllm_config())
+            except (ImportError, AttributeError, TypeError):
+                pass
 
     def fused_output_quant_supported(self, quant_key):
         return False
@@ -314,9 +362,16 @@ class Gfx906FAImpl(AttentionImpl):
         gfx906_fa.rope_and_cache_q8_kv(pos, q, k, v, cos_sin_cache, is_neox, sm, kp, vp)
 
     @classmethod
+    def bound_bytes(cls, heads, limits: tuple[int, int, int]) -> int:
+        """The workspace every batch within the scheduler limits needs, plus
+        the tile-image room up to image_room_bytes()."""
+        max_seqs, max_tokens, max_len = limits
+        return workspace_upper_bound(max_seqs, max_tokens, heads, max_len, image_room_bytes())
+
+    @classmethod
     def reserve_workspace(cls, nbytes: int, device: torch.device) -> torch.Tensor:
         """Grow the shared workspace to at least nbytes (never shrinks; grows
-        by at least a quarter, so few buffers are ever retired)."""
+        by at least a quarter, so few buffers are ever replaced)."""
         ws = cls._workspace
         if ws is None or ws.numel() < nbytes or ws.device != device:
             if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
@@ -326,6 +381,8 @@ class Gfx906FAImpl(AttentionImpl):
             size = nbytes
             if ws is not None and ws.device == device:
                 size = max(nbytes, ws.numel() + ws.numel() // 4)
+            if ws is not None and not cls._captured:
+                cls._workspace = ws = None  # free it before the larger one is made
             new = gfx906_fa.new_workspace(size, device)
             if ws is not None:
                 cls._retired.append(ws)
@@ -353,16 +410,24 @@ class Gfx906FAImpl(AttentionImpl):
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("GFX906_FA: output quantization is not supported")
         if attn_metadata is None:
-            # Profiling run.
+            # Profiling run: reserve the workspace bound here, so that vLLM's
+            # memory profile (which sizes the KV cache) counts it.
+            if self._limits is not None and query is not None and query.device.type == "cuda":
+                heads = set(self._layer_heads) | {(self.num_heads, self.num_kv_heads)}
+                self.reserve_workspace(self.bound_bytes(heads, self._limits), query.device)
             return output.fill_(0)
         assert not attn_metadata.use_cascade, "GFX906_FA: cascade is not supported"
         n = attn_metadata.num_actual_tokens
         kp, vp = q8_planes(kv_cache, self.num_kv_heads, self.head_size)
         md = attn_metadata
         B = md.seq_lens.shape[0]
+        if torch.cuda.is_current_stream_capturing():
+            Gfx906FAImpl._captured = True
+        # the regions the call needs; tile images use whatever room the
+        # reserved workspace has past them
         ws = self._get_workspace(
-            gfx906_fa.workspace_size(B, n, self.num_heads, self.num_kv_heads, md.max_query_len,
-                                     md.max_seq_len), query.device)
+            gfx906_fa.plan_info(B, n, self.num_heads, self.num_kv_heads, md.max_query_len,
+                                md.max_seq_len, self.head_size)["img_offset"], query.device)
         out = output[:n].view(n, self.num_heads, self.head_size)
         forward_paged(query[:n], kp, vp, md.block_table, md.seq_lens, md.query_start_loc,
                       md.max_query_len, md.max_seq_len, self.scale, out=out, workspace=ws)

@@ -244,6 +244,19 @@ int gfx906_fa_amd_paged_attention_plan_info(int num_seqs, int num_tokens, int nu
                                             int num_kv_heads, int head_size, int max_query_len,
                                             int max_seq_len, int64_t *info, int info_len);
 
+/* (5-bound-info) The bound of (5-bound) in its two parts: info[0] the
+ *     regions every call of those limits needs (each call's plan_info()
+ *     img_offset is at most this), info[1] the room for prefill tile
+ *     images of contexts up to max_seq_len keys (max_seq_len <= 0: any
+ *     context, the library's 1 GiB cap).  The image room is optional: a
+ *     workspace of info[0] bytes runs every such call, whose prefill
+ *     workgroups then dequantize their own tiles where images do not fit.
+ *     Returns 2 (at most info_len entries written) or -1 for an invalid
+ *     shape.  No reference counterpart. */
+int gfx906_fa_amd_paged_attention_workspace_bound_info(int max_num_seqs, int64_t max_num_tokens, int num_heads,
+                                                       int num_kv_heads, int head_size, int64_t max_seq_len,
+                                                       int64_t *info, int info_len);
+
 /* Compute units of the current device the plans are made for (256, the
  * MI355X count, when no device is visible).  No reference counterpart. */
 int gfx906_fa_amd_device_cus(void);

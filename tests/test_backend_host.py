@@ -174,21 +174,72 @@ def test_graph_support_and_workspace_bound():
                     continue
                 T = rng.randint(n, max_tokens)
                 shapes.append((n, T, rng.randint(1, T - n + 1)))
+            info = gfx906_fa.workspace_bound_info(max_seqs, max_tokens, hq, hkv)
+            assert info["regions"] + info["img_bytes"] == bound
             for n, T, mq in shapes:
                 # long and short contexts: the decode classes differ (48-row
                 # tiles only with enough sub-pages per workgroup)
                 for msl in (1 << 17, 2048):
                     need = gfx906_fa.workspace_size(n, T, hq, hkv, mq, msl)
                     assert need <= bound, (hq, hkv, max_seqs, max_tokens, n, T, mq, msl, need, bound)
+                    # the regions alone run every call (the image room is optional)
+                    reg = gfx906_fa.plan_info(n, T, hq, hkv, mq, msl)["img_offset"]
+                    assert reg <= info["regions"], (hq, hkv, max_seqs, max_tokens, n, T, mq, msl)
     # several layer shapes: the largest bound
     both = workspace_upper_bound(64, 4096, [(48, 8), (6, 1)])
     assert both == max(gfx906_fa.workspace_bound(64, 4096, 48, 8), gfx906_fa.workspace_bound(64, 4096, 6, 1))
 
 
+def test_bound_image_room_follows_max_model_len_and_the_cap(monkeypatch):
+    """The image part of the bound shrinks with max_model_len and is capped
+    by GFX906_FA_IMAGE_ROOM_MB; the regions part is independent of both."""
+    import gfx906_fa
+    from gfx906_fa_backend import image_room_bytes, workspace_upper_bound
+    full = gfx906_fa.workspace_bound_info(16, 8192, 48, 8)
+    short = gfx906_fa.workspace_bound_info(16, 8192, 48, 8, max_seq_len=4096)
+    # up to 16 prefill sequences of 4096 keys: 64 tiles x 8 kv-heads x 35840 B each
+    assert full["img_bytes"] == 1 << 30 and short["img_bytes"] == 16 * 64 * 8 * 35840
+    assert short["regions"] == full["regions"]
+    monkeypatch.delenv("GFX906_FA_IMAGE_ROOM_MB", raising=False)
+    assert image_room_bytes() == 256 << 20
+    monkeypatch.setenv("GFX906_FA_IMAGE_ROOM_MB", "0")
+    assert image_room_bytes() == 0
+    assert workspace_upper_bound(16, 8192, [(48, 8)], -1, 0) == full["regions"]
+    assert workspace_upper_bound(16, 8192, [(48, 8)], -1, 100 << 20) == full["regions"] + (100 << 20)
+    assert workspace_upper_bound(16, 8192, [(48, 8)], 4096, 1 << 30) == short["regions"] + short["img_bytes"]
+
+
+def test_profiling_forward_reserves_the_bound(monkeypatch):
+    """vLLM sizes the KV cache from the memory its profiling run used, so the
+    profiling forward (attn_metadata None) reserves the workspace bound of
+    the scheduler limits (taken from the current vLLM config at model
+    construction) on the device."""
+    import types
+    import gfx906_fa_backend as GB
+    from gfx906_fa_backend import Gfx906FAImpl
+    from vllm.config import set_current_vllm_config
+    monkeypatch.setattr(Gfx906FAImpl, "_limits", None)
+    monkeypatch.setattr(Gfx906FAImpl, "_layer_heads", set())
+    asked = []
+    monkeypatch.setattr(Gfx906FAImpl, "reserve_workspace",
+                        classmethod(lambda cls, n, dev: asked.append((n, dev.type))))
+    cfg = types.SimpleNamespace(scheduler_config=types.SimpleNamespace(max_num_seqs=64, max_num_batched_tokens=4096),
+                                model_config=types.SimpleNamespace(max_model_len=32768))
+    with set_current_vllm_config(cfg):
+        impl = Gfx906FAImpl(48, 128, 0.1, 8, None, None, "auto")
+    assert Gfx906FAImpl._limits == (64, 4096, 32768)
+    out = torch.ones(3, 48 * 128)
+    fake_q = types.SimpleNamespace(device=torch.device("cuda"))
+    assert impl.forward(None, fake_q, None, None, None, None, output=out) is out and not out.any()
+    assert asked == [(Gfx906FAImpl.bound_bytes({(48, 8)}, (64, 4096, 32768)), "cuda")]
+    assert asked[0][0] == GB.workspace_upper_bound(64, 4096, [(48, 8)], 32768, GB.image_room_bytes())
+
+
 def test_builder_reserves_the_bound_and_retires_workspaces(monkeypatch):
     """The builder reserves the bound for the scheduler limits and the layer
-    shapes; a larger request later replaces the workspace but keeps the old
-    one alive (a captured graph may still write into it)."""
+    shapes; a larger request later replaces the workspace.  Before any graph
+    capture the old one is freed; after a capture it is kept alive (a
+    captured graph may still write into it)."""
     import types
     import gfx906_fa
     import gfx906_fa_backend as GB
@@ -204,7 +255,9 @@ def test_builder_reserves_the_bound_and_retires_workspaces(monkeypatch):
     monkeypatch.setattr(gfx906_fa, "new_workspace", fake_new_workspace)
     monkeypatch.setattr(Gfx906FAImpl, "_workspace", None)
     monkeypatch.setattr(Gfx906FAImpl, "_retired", [])
+    monkeypatch.setattr(Gfx906FAImpl, "_captured", False)
     monkeypatch.setattr(Gfx906FAImpl, "_layer_heads", set())
+    monkeypatch.setattr(Gfx906FAImpl, "_limits", None)
     Gfx906FAImpl(48, 128, 0.1, 8, None, None, "auto")
     Gfx906FAImpl(6, 128, 0.1, 1, None, None, "auto")
     cfg = types.SimpleNamespace(scheduler_config=types.SimpleNamespace(max_num_seqs=128,
@@ -219,8 +272,20 @@ def test_builder_reserves_the_bound_and_retires_workspaces(monkeypatch):
     assert Gfx906FAImpl.reserve_workspace(want // 2, cpu) is first      # never shrinks
     second = Gfx906FAImpl.reserve_workspace(want + 1, cpu)
     assert second is not first and second.numel() >= want + want // 4  # grows by a quarter at least
-    assert Gfx906FAImpl._retired == [first]                              # the old one stays alive
+    assert Gfx906FAImpl._retired == []                                   # no capture yet: freed
     assert GB.Gfx906FAImpl._workspace is second
+    # a capture from the builder: replaced workspaces now stay alive
+    from vllm.v1.attention.backend import CommonAttentionMetadata
+    b = Gfx906FAMetadataBuilder(AttentionSpec(block_size=16, num_kv_heads=8), ["l0"], cfg, cpu)
+    md = CommonAttentionMetadata(query_start_loc=torch.tensor([0, 1], dtype=torch.int32),
+                                 seq_lens=torch.tensor([5], dtype=torch.int32), num_reqs=1,
+                                 num_actual_tokens=1, max_query_len=1, max_seq_len=5,
+                                 block_table_tensor=torch.zeros(1, 1, dtype=torch.int32),
+                                 slot_mapping=torch.zeros(1, dtype=torch.int64))
+    b.build_for_cudagraph_capture(md)
+    assert Gfx906FAImpl._captured
+    third = Gfx906FAImpl.reserve_workspace(second.numel() + 1, cpu)
+    assert third is not second and Gfx906FAImpl._retired == [second]
 
 
 def test_forward_debug_log_records_the_call_and_its_failure(tmp_path, monkeypatch):

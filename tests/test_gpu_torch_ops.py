@@ -170,3 +170,26 @@ def test_compiled_step_matches_eager(batch):
     torch._dynamo.reset()
     assert torch.equal(c_eager, c_comp)
     assert torch.equal(eager, comp)
+
+
+def test_paged_attention_out_op_takes_workspace_without_image_room():
+    """A 2048-token prompt at 48/8 has room for 64-key tile images in its
+    workspace_size(); the out-variant op accepts a workspace of only the
+    regions every call needs (plan_info ``img_offset``), as the function
+    does, and gives the same output bit for bit (its prefill workgroups then
+    dequantize their own tiles); one byte less is refused."""
+    announce("torch op paged_attention_out, img_offset workspace")
+    b = W.build_batch([2048], [2048], 48, 8, dtype="bf16", seed=13, device="cuda")
+    info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len)
+    assert info["img_bytes"] > 0
+    full = gfx906_fa.new_workspace(info["bytes"], b.device)
+    small = gfx906_fa.new_workspace(info["img_offset"], b.device)
+    o_full = torch.empty_like(b.query)
+    o_small = torch.empty_like(b.query)
+    OPS.paged_attention_out(*_attn_args(b), o_full, full)
+    OPS.paged_attention_out(*_attn_args(b), o_small, small)
+    torch.cuda.synchronize()
+    assert torch.equal(o_full, o_small)
+    short = gfx906_fa.new_workspace(info["img_offset"] - 256, b.device)
+    with pytest.raises(RuntimeError, match="workspace needs"):
+        OPS.paged_attention_out(*_attn_args(b), o_small, short)

@@ -60,3 +60,38 @@ def test_large_values_within_scaled_bound(case):
     assert vmax > 3 * vs and kmax > 3 * ks  # the draws reached the scales
     atol = 2e-3 * max(1.0, vmax / 4) * (max(1.0, kmax / 4) if ks > 1 else 1.0)
     assert_close(got, ref, atol=atol)
+
+
+BIG_K = [
+    # name, seq_lens, q_lens, Hq, Hkv
+    ("fresh200_8x8", [200], [200], 8, 8),
+    ("chunk20_ctx2k_48x8", [2000 + 20], [20], 48, 8),
+    ("mixed_decode_48x8", [3000, 900 + 150, 500], [1, 150, 1], 48, 8),
+]
+
+
+@pytest.mark.parametrize("case", BIG_K, ids=[c[0] for c in BIG_K])
+def test_keys_near_fp16_limit(case):
+    """Keys up to 60000 at a softmax scale whose c = scale * log2 e has a
+    mantissa near 1 (0.0858: c = 0.99 * 2^-3).  The prefill kernel's K^ =
+    fp16(q * d_k * kmul) must stay finite wherever the decode kernel's
+    fp16(q * d_k) is, so kmul is kept in [0.5, 1).  Queries at 5e-4 x N(0, 1)
+    keep the scores at a few units; their error, and the bound, scale with
+    the score magnitude."""
+    need_gpu()
+    name, sls, qls, Hq, Hkv = case
+    announce(f"big keys {name}")
+    b = W.build_batch(sls, qls, Hq, Hkv, seed=sum(map(ord, name)), write_cache=False)
+    b.key = (b.key.float() * 12000).clamp(-60000, 60000).to(b.key.dtype)
+    b.query = (b.query.float() * 5e-4).to(b.query.dtype)
+    b.scale = 0.0858
+    kp, vp = b.planes()
+    import gfx906_fa
+    gfx906_fa.reshape_and_cache_q8_kv(b.key, b.value, b.slot_mapping, kp, vp)
+    out = W.attention(b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert float(b.key.float().abs().max()) > 40000
+    # score magnitude: |q| |k| scale over the head dim
+    s_std = float(b.query.float().std() * b.key.float().std()) * 128 ** 0.5 * b.scale
+    assert 1.0 < s_std < 20.0, s_std
+    assert_close(to_np_f32(out), batch_oracle(b), atol=2e-3 * max(1.0, s_std))
