@@ -40,7 +40,10 @@ Also reported on the same JSON line:
                   model-dtype copies timed at cfg3's output size (here the
                   kernels write the model dtype in place); prefix chunks:
                   short prefills on long cached prefixes (their row tiles
-                  split over the keys), per pass.
+                  split over the keys), per pass; reference_matrix: the
+                  reference benchmark's own decode and prefill shapes through
+                  the contiguous forward (and the decode ones through
+                  paged_attention).
   cpu_baseline  - the reference's PyTorch CPU path (oracle/cpu_baseline.py)
                   on the host cores this process may use (its affinity mask,
                   capped by OMP_NUM_THREADS; the count is in ``cores``):
@@ -222,6 +225,64 @@ def prefix_chunk_times(dev) -> dict:
         res[name] = {"us": round(ms * 1e3, 1), "tflops": round(b.flops() / (ms * 1e-3) / 1e12, 1),
                      "cache_gbs": round(b.kv_bytes() / (ms * 1e-3) / 1e9, 1)}
         del b, o, ws
+        torch.cuda.empty_cache()
+    return res
+
+
+# The reference's own benchmark matrix (tests/bench.py:39-66 of the
+# reference): gfx906_fa.forward(q fp32, AoS Q8_0 K, fp16 V, scale) at batch 1,
+# no mask, non-causal.
+REF_DECODE = [("dec_128", 8, 4, 128), ("dec_512", 8, 4, 512), ("dec_1k", 8, 4, 1024), ("dec_4k", 8, 4, 4096),
+              ("dec_8k", 8, 4, 8192), ("dec_16k", 8, 4, 16384), ("dec_32k", 8, 4, 32768),
+              ("dec_64k", 8, 4, 65536), ("dec_94k", 8, 4, 94208), ("dec_128k", 8, 4, 131072),
+              ("mmx_dec_1k", 48, 8, 1024), ("mmx_dec_8k", 48, 8, 8192), ("mmx_dec_32k", 48, 8, 32768),
+              ("mmx_dec_94k", 48, 8, 94208)]
+REF_PREFILL = [("pre_512", 8, 4, 512), ("pre_1k", 8, 4, 1024), ("pre_2k", 8, 4, 2048), ("pre_4k", 8, 4, 4096),
+               ("pre_8k", 8, 4, 8192)]
+
+
+def reference_matrix(dev) -> dict:
+    """The reference benchmark's shapes through the contiguous ``forward``
+    (device time per call from HIP events: the call's kernels and its q / out
+    transposes, not the host launch cost), and each decode shape also through
+    ``paged_attention`` on a Q8_0 paged cache (block_size 16, permuted table).
+    Decode GB/s counts the bytes each path must read and write: forward the
+    AoS K (136 B) and fp16 V (256 B) per key and kv-head, paged the Q8 K and
+    V (272 B); prefill TFLOP/s counts 4 * D * Hq * Sq * Skv (non-causal)."""
+    import torch
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+    res = {"workload": "B = 1, D = 128, fp32 q, scale 1/sqrt(128); forward: AoS Q8_0 K + fp16 V, no mask; "
+                       "paged: Q8_0 K + V pages, fp16 q and out"}
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    for name, hq, hkv, skv in REF_DECODE:
+        q = torch.randn((1, hq, 1, 128), generator=g, device=dev)
+        k = torch.randn((1, hkv, skv, 128), generator=g, device=dev).mul_(0.1).half()
+        v = torch.randn((1, hkv, skv, 128), generator=g, device=dev).mul_(0.1).half()
+        kq = gfx906_fa.quantize_q8_0(k)
+        del k
+        ms = timed(lambda: gfx906_fa.forward(q, kq, v, 1.0 / 128 ** 0.5), 50, 10)
+        fbytes = hkv * skv * (136 + 256) + 2 * hq * 128 * 4
+        b = W.build_batch([skv], [1], hq, hkv, seed=1, device=dev, host_values=False)
+        o = torch.empty((1, hq, 128), dtype=torch.float16, device=dev)
+        ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(1, 1, hq, hkv, 1, skv), dev)
+        ms_p = timed(_attn_fn(b, o, ws), 50, 10)
+        res[name] = {"heads": f"{hq}/{hkv}", "skv": skv, "forward_us": round(ms * 1e3, 1),
+                     "forward_gbs": round(fbytes / (ms * 1e-3) / 1e9, 1), "paged_us": round(ms_p * 1e3, 1),
+                     "paged_gbs": round(b.hbm_bytes(2) / (ms_p * 1e-3) / 1e9, 1)}
+        del q, kq, v, b, o, ws
+        torch.cuda.empty_cache()
+    for name, hq, hkv, sq in REF_PREFILL:
+        q = torch.randn((1, hq, sq, 128), generator=g, device=dev)
+        k = torch.randn((1, hkv, sq, 128), generator=g, device=dev).mul_(0.1).half()
+        v = torch.randn((1, hkv, sq, 128), generator=g, device=dev).mul_(0.1).half()
+        kq = gfx906_fa.quantize_q8_0(k)
+        ms = timed(lambda: gfx906_fa.forward(q, kq, v, 1.0 / 128 ** 0.5), 20, 5)
+        fl = 4.0 * 128 * hq * sq * sq
+        res[name] = {"heads": f"{hq}/{hkv}", "sq": sq, "skv": sq, "forward_us": round(ms * 1e3, 1),
+                     "forward_tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+        del q, k, kq, v
         torch.cuda.empty_cache()
     return res
 
@@ -597,7 +658,8 @@ def main() -> int:
         res["next_rows"] = {"graph_replay": graph,
                             "output_epilogue": output_epilogue_ms(dev),
                             "prefix_chunks": prefix_chunk_times(dev),
-                            "gather": gather_rates(dev)}
+                            "gather": gather_rates(dev),
+                            "reference_matrix": reference_matrix(dev)}
 
     if args.calib_copy_mib:
         # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE

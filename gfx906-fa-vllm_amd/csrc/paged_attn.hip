@@ -2245,6 +2245,281 @@ __global__ __launch_bounds__(256) void attn_prefill_combine_kernel(AttnParams p)
 }
 
 // ---------------------------------------------------------------------------
+// Contiguous decode: the op module's forward() for rows (Sq * G per kv-head)
+// that fit one 16-row group, with no mask.  It reads the reference's
+// contiguous layouts as they are (extension/gfx906_fa.cpp:120-265): K as
+// AoS Q8_0 rows [B][Hkv][Skv][136 B], V as fp16 rows [B][Hkv][Skv][128], so
+// no repacking pass runs.  A segment is one (batch, kv-head); its 16-token
+// sub-pages are cut into P equal pieces, one single-wave workgroup each
+// (grid B * Hkv * P).  A piece streams its sub-pages through a 3-slot LDS
+// ring, two sub-pages ahead (global_load_lds copies: 2176 B of K rows, 4096
+// B of V rows), and computes as the decode kernel's one-row-group tile:
+//   S^T = K^ . Q^T   4 x mfma 16x16x32, K^ = fp16(q * d_k) per lane from its
+//                    token's AoS row (8 int8 of block b at 34b + 2 + 8g);
+//   O^T += V^T . P^T 8 x mfma 16x16x16, V exact in fp16 (lane (i, g) reads
+//                    d = 16m + i of tokens 4g..4g+3), P unscaled.
+// With P = 1 the piece writes the normalized output, else (m, l, O) for
+// flat_combine_kernel.  A segment's K rows start 8 bytes past a 16-byte
+// boundary when seg * Skv is odd (136-byte rows, a 16-byte aligned tensor):
+// the copies then start at the boundary below (koff = 8), and the K region
+// of a slot has room for the extra bytes.  A segment's last sub-page is read
+// with guarded dword loads (zeros past Skv), so no copy reads past a
+// segment's rows (nor, for the first segment, before them: koff = 0).
+constexpr int FD_KROWS = 16 * 136;             // K rows of a sub-page
+constexpr int FD_KREG = FD_KROWS + 16;         // their slot region (koff + rows, 16-byte multiple)
+constexpr int FD_SLOT = FD_KREG + 16 * 256;    // then the V rows
+constexpr int FD_RING = 3;
+constexpr int FD_DMA = 7;                      // copies per sub-page: K 2 + 1 partial, V 4
+constexpr int FD_ROW = 132;                    // partial row: m, l, 2 pad, O[128] (floats)
+static_assert(FD_KROWS == 2 * 1024 + 128 && FD_KREG == 2 * 1024 + 9 * 16, "K: two full copies, 8 or 9 lanes");
+
+struct FlatParams {
+    const void *q;
+    int64_t q_ts, q_hs;
+    const uint8_t *k;       // AoS Q8_0 rows, [B * Hkv * Skv][136]
+    const uint8_t *v;       // fp16 rows, [B * Hkv * Skv][256 B]
+    const int32_t *kv_len;  // [B]: keys each batch row sees (clamped to [0, Skv])
+    const int32_t *q_abs;   // [B] or nullptr: row j sees keys <= q_abs[b] + j
+    int B, Hkv, G, Sq, Skv, P, nsp;
+    float c;                // scale * log2 e
+    float *out;             // fp32 [B * Sq][Hq][128]
+    int64_t o_ts, o_hs;
+    float *ws;              // partials [segment][piece][Sq * G rows][FD_ROW]
+};
+
+__device__ __forceinline__ uint32_t lds32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+
+template <int QDT>
+__global__ __launch_bounds__(64) void flat_decode_kernel(FlatParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[FD_RING * FD_SLOT];
+    const int lane = threadIdx.x, i16 = lane & 15, g = lane >> 4;
+    const int seg = blockIdx.x / p.P, pc = blockIdx.x - seg * p.P;
+    const int b = seg / p.Hkv, h = seg - b * p.Hkv;
+    const int kvl = min(max(p.kv_len[b], 0), p.Skv);
+    const int s0 = (int)((int64_t)pc * p.nsp / p.P);
+    const int s1 = min((int)((int64_t)(pc + 1) * p.nsp / p.P), (kvl + 15) >> 4);
+    const int n = max(s1 - s0, 0);
+    const int nrows = p.Sq * p.G;
+    // the lane's query row i16 (token i16 / G, q-head h * G + i16 % G)
+    half8_t qf[4];
+    int lim = INT32_MAX;
+    const int jr = i16 / p.G;
+    const int hq = h * p.G + (i16 - jr * p.G);
+    if (i16 < nrows) {
+        const int64_t qoff = (int64_t)(b * p.Sq + jr) * p.q_ts + (int64_t)hq * p.q_hs + 8 * g;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) qf[bb] = load_q8<QDT>(p.q, qoff + 32 * bb);
+        lim = p.q_abs ? min(kvl - 1, p.q_abs[b] + jr) : kvl - 1;
+    } else {
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) qf[bb] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    int lim_min;
+    {
+        const float f = (float)min(lim, 1 << 24);
+        lim_min = __builtin_amdgcn_readfirstlane((int)(-row16_max(xrow_max(-f))));
+    }
+    float4_t o[8];
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) o[mm] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    const float c = p.c;
+    const int64_t rows0 = (int64_t)seg * p.Skv;  // the segment's first row
+    const uint8_t *kseg = p.k + rows0 * 136;
+    const uint8_t *vseg = p.v + rows0 * 256;
+    const int koff = (int)(rows0 & 1) * 8;       // kseg is 8 bytes past a 16-byte boundary for odd rows0
+    const int last_sp = p.nsp - 1;               // the segment's last sub-page (guarded loads)
+    const uint32_t ring_lds =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring);
+
+    // sub-page j of the piece into slot sl (K rows at koff, V rows at
+    // FD_KREG): FD_DMA copies, or for the segment's last sub-page guarded
+    // dword loads stored to LDS, after which every earlier copy has landed
+    // too (loads complete in order)
+    auto fetch = [&](int j, int sl) __attribute__((always_inline)) {
+        if (j >= n) return;  // uniform
+        const int sp = s0 + j, tok0 = 16 * sp;
+        const uint32_t dk = ring_lds + sl * FD_SLOT, dv = dk + FD_KREG;
+        if (sp != last_sp) {  // uniform: 16 rows, and the 16-byte runs copied stay inside the segment
+            const uint8_t *kb = kseg + (int64_t)tok0 * 136 - koff + 16 * lane;
+            const uint8_t *vb = vseg + (int64_t)tok0 * 256 + 16 * lane;
+            lds_dma16<true>(kb, dk);
+            lds_dma16<true>(kb + 1024, dk + 1024);
+            lds_dma16<true>(vb, dv);
+            lds_dma16<true>(vb + 1024, dv + 1024);
+            lds_dma16<true>(vb + 2048, dv + 2048);
+            lds_dma16<true>(vb + 3072, dv + 3072);
+            if (16 * lane < FD_KROWS + koff - 2048) lds_dma16<true>(kb + 2048, dk + 2048);
+        } else {
+            const int nt = min(p.Skv - tok0, 16);  // valid rows
+            const uint32_t *ksrc = reinterpret_cast<const uint32_t *>(kseg + (int64_t)tok0 * 136);
+            const uint32_t *vsrc = reinterpret_cast<const uint32_t *>(vseg + (int64_t)tok0 * 256);
+            uint32_t *kd = reinterpret_cast<uint32_t *>(ring + sl * FD_SLOT + koff);
+            uint32_t *vd = reinterpret_cast<uint32_t *>(ring + sl * FD_SLOT + FD_KREG);
+            for (int i = lane; i < FD_KROWS / 4; i += 64) kd[i] = i < nt * 34 ? ksrc[i] : 0u;
+            for (int i = lane; i < 16 * 64; i += 64) vd[i] = i < nt * 64 ? vsrc[i] : 0u;
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        }
+    };
+    auto landed = [&](int j) __attribute__((always_inline)) {
+        static_assert(FD_DMA * (FD_RING - 1) <= 63, "vmcnt immediate");
+        if (j + FD_RING - 1 < n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FD_DMA * (FD_RING - 1)) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    // one sub-page from slot sb (tokens tok0 .. tok0 + 15)
+    auto attend = [&](const uint8_t *sb, int tok0) __attribute__((always_inline)) {
+        half8_t ka[4];
+        const uint8_t *krow = sb + koff + i16 * 136;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const uint8_t *blk = krow + 34 * bb;  // 4-byte aligned for even bb, else 2 past
+            uint32_t w0, w1, dsc;
+            if ((bb & 1) == 0) {  // ints at blk + 2 + 8g: 2 bytes past a dword
+                const uint32_t d0 = lds32(blk + 8 * g), d1 = lds32(blk + 8 * g + 4), d2 = lds32(blk + 8 * g + 8);
+                w0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+                w1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+                dsc = lds32(blk) & 0xFFFFu;
+            } else {              // ints at blk + 2 + 8g: dword aligned
+                w0 = lds32(blk + 2 + 8 * g);
+                w1 = lds32(blk + 6 + 8 * g);
+                dsc = lds32(blk - 2) >> 16;
+            }
+            const half_t d = __builtin_bit_cast(half_t, (uint16_t)dsc);
+            const half8_t dd = {d, d, d, d, d, d, d, d};
+            ka[bb] = i8x8_to_half8(w0, w1) * dd;
+        }
+        float4_t sacc = mfma16(ka[0], qf[0], float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int bb = 1; bb < 4; ++bb) sacc = mfma16(ka[bb], qf[bb], sacc);
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = sacc[i];  // token tok0 + 4g + i
+        if (!(tok0 + 16 <= kvl && tok0 + 15 <= lim_min)) {  // uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = tok0 + 4 * g + i;
+                sv[i] = (key < kvl && key <= lim) ? sv[i] : -INFINITY;
+            }
+        }
+        const float mt = xrow_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
+        const bool need = mt > m + LAZY_TAU;
+        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after warm-up
+            const float mn = need ? mt : m;
+            const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm) o[mm] *= alpha;
+        }
+        const float nms = m == -INFINITY ? 0.0f : -m;
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], c, nms));
+        l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        const half4_t pb = {(half_t)pr[0], (half_t)pr[1], (half_t)pr[2], (half_t)pr[3]};
+        const uint16_t *vt = reinterpret_cast<const uint16_t *>(sb + FD_KREG) + (4 * g) * 128 + i16;
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) {
+            half4_t va;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) va[e] = __builtin_bit_cast(half_t, vt[e * 128 + 16 * mm]);
+            o[mm] = mfma16k16(va, pb, o[mm]);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < FD_RING - 1; ++u) fetch(u, u);
+    for (int base = 0; base < n; base += FD_RING) {
+#pragma unroll
+        for (int u = 0; u < FD_RING; ++u) {
+            const int j = base + u;
+            if (j < n) {  // uniform
+                // the previous step's reads of the slot refilled next have completed
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                fetch(j + FD_RING - 1, (u + FD_RING - 1) % FD_RING);
+                landed(j);
+                attend(ring + u * FD_SLOT, 16 * (s0 + j));
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    l = xrow_sum(l);
+    if (i16 >= nrows) return;
+    if (p.P == 1) {  // the whole segment: normalized output
+        const float inv = l > 0.f ? 1.0f / l : 0.0f;
+        float *ob = p.out + (int64_t)(b * p.Sq + jr) * p.o_ts + (int64_t)hq * p.o_hs + 4 * g;
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) *reinterpret_cast<float4_t *>(ob + 16 * mm) = o[mm] * inv;
+    } else {
+        float *row = p.ws + (((int64_t)seg * p.P + pc) * nrows + i16) * FD_ROW;
+        if (g == 0) *reinterpret_cast<float2_t *>(row) = float2_t{m, l};
+#pragma unroll
+        for (int mm = 0; mm < 8; ++mm) *reinterpret_cast<float4_t *>(row + 4 + 16 * mm + 4 * g) = o[mm];
+    }
+}
+
+// Merges the P pieces of each (segment, row): grid (B * Hkv, Sq * G), 256
+// threads.  Thread t owns d-chunk t % 32 (4 d) and pieces t / 32, t / 32 + 8,
+// ... (one-pass online merge, four pieces' loads in flight); the 8 partial
+// states per d-chunk are merged through LDS.
+__global__ __launch_bounds__(256) void flat_combine_kernel(FlatParams p) {
+    __shared__ float sm_m[8], sm_l[8];
+    __shared__ float4_t sm_o[8][32];
+    const int seg = blockIdx.x, r = blockIdx.y;
+    const int nrows = p.Sq * p.G;
+    const int t = threadIdx.x, grp = t >> 5, d0 = 4 * (t & 31);
+    float M = -INFINITY, L = 0.f;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const float *base = p.ws + ((int64_t)seg * p.P * nrows + r) * FD_ROW;
+    const int64_t pstep = (int64_t)nrows * FD_ROW;  // piece k -> k + 1
+    for (int k0 = grp; k0 < p.P; k0 += 32) {
+        float2_t ml[4];
+        float4_t oc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int k = k0 + 8 * u;
+            const float *row = base + k * pstep;
+            ml[u] = k < p.P ? *reinterpret_cast<const float2_t *>(row) : float2_t{-INFINITY, 0.f};
+            oc[u] = k < p.P ? *reinterpret_cast<const float4_t *>(row + 4 + d0) : float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float mc = ml[u][0];
+            if (mc > -INFINITY) {
+                const float mn = fmaxf(M, mc);
+                const float a = __builtin_amdgcn_exp2f(M - mn);  // 0 while M is -inf
+                const float bw = __builtin_amdgcn_exp2f(mc - mn);
+                L = fmaf(L, a, bw * ml[u][1]);
+                acc = acc * a + bw * oc[u];
+                M = mn;
+            }
+        }
+    }
+    if ((t & 31) == 0) {
+        sm_m[grp] = M;
+        sm_l[grp] = L;
+    }
+    sm_o[grp][t & 31] = acc;
+    __syncthreads();
+    if (grp != 0) return;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, sm_m[k]);
+    const float ms = mx == -INFINITY ? 0.0f : mx;
+    float l = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float wk = sm_m[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm_m[k] - ms);
+        l = fmaf(sm_l[k], wk, l);
+        o += sm_o[k][t & 31] * wk;
+    }
+    const int b = seg / p.Hkv, h = seg - b * p.Hkv;
+    const int j = r / p.G, hq = h * p.G + (r - j * p.G);
+    const float inv = l > 0.f ? 1.0f / l : 0.0f;
+    *reinterpret_cast<float4_t *>(p.out + (int64_t)(b * p.Sq + j) * p.o_ts + (int64_t)hq * p.o_hs + d0) = o * inv;
+}
+
+// ---------------------------------------------------------------------------
 // Host-side plan.  Deterministic in the call's scalar arguments and the
 // device's CU count, so that workspace_size() and the launch agree.
 //
@@ -2879,6 +3154,90 @@ extern "C" hipError_t gfx906_fa_amd_paged_attention_kv_write(
                                 num_heads, num_kv_heads, head_size, block_size, max_query_len, max_seq_len,
                                 scale, out, out_dtype, out_token_stride, out_head_stride, workspace,
                                 workspace_bytes, &nkv, stream);
+}
+
+namespace {
+
+// Pieces per segment of the contiguous decode: enough single-wave
+// workgroups to fill the device (8 per CU), each at least FD_MIN_SUB
+// sub-pages (its fixed costs - Q load, ring fill, partial write - stay
+// small against its stream).
+#ifndef GFA_FD_MIN_SUB
+#define GFA_FD_MIN_SUB 8
+#endif
+int flat_pieces(int nseg, int nsp) {
+    const int64_t target = (int64_t)device_cus() * 8;
+    const int64_t want = (target + nseg - 1) / max(nseg, 1);
+    const int64_t most = max(nsp / GFA_FD_MIN_SUB, 1);
+    return (int)max((int64_t)1, min(want, most));
+}
+
+}  // namespace
+
+extern "C" size_t gfx906_fa_amd_flat_decode_workspace_size(int batch, int seq_q, int num_heads, int num_kv_heads,
+                                                          int seq_kv) {
+    if (batch <= 0 || seq_q <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads || seq_kv <= 0)
+        return 256;
+    const int nseg = batch * num_kv_heads, nsp = (seq_kv + 15) / 16;
+    const int P = flat_pieces(nseg, nsp);
+    const size_t rows = (size_t)seq_q * (num_heads / num_kv_heads);
+    return P > 1 ? align256((size_t)nseg * P * rows * FD_ROW * sizeof(float)) : 256;
+}
+
+extern "C" hipError_t gfx906_fa_amd_flat_decode(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride, const uint8_t *k_q8,
+    const void *v_f16, const int32_t *kv_len, const int32_t *q_abs_offset, int batch, int seq_q, int num_heads,
+    int num_kv_heads, int seq_kv, int head_size, float scale, float *out, int64_t out_token_stride,
+    int64_t out_head_stride, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (batch == 0 || seq_q == 0 || seq_kv == 0) return hipSuccess;
+    const int G = (num_kv_heads > 0 && num_heads > 0) ? num_heads / num_kv_heads : 0;
+    if (head_size != 128 || G <= 0 || num_heads % num_kv_heads || batch < 0 || seq_q < 0 || seq_kv < 0 ||
+        (int64_t)seq_q * G > 16 || q_dtype < 0 || q_dtype > 2 || kv_len == nullptr) {
+        fprintf(stderr, "[gfx906_fa_amd] flat_decode: unsupported configuration (head_size=%d heads=%d/%d seq_q=%d: "
+                        "seq_q * heads/kv_heads must be <= 16; kv_len required)\n",
+                head_size, num_heads, num_kv_heads, seq_q);
+        return hipErrorInvalidValue;
+    }
+    if (((uintptr_t)k_q8 | (uintptr_t)v_f16) & 15u) {
+        fprintf(stderr, "[gfx906_fa_amd] flat_decode: K and V bases must be 16-byte aligned\n");
+        return hipErrorInvalidValue;
+    }
+    const size_t need = gfx906_fa_amd_flat_decode_workspace_size(batch, seq_q, num_heads, num_kv_heads, seq_kv);
+    const int nseg = batch * num_kv_heads, nsp = (seq_kv + 15) / 16;
+    const int P = flat_pieces(nseg, nsp);
+    if (P > 1 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 15u))) {
+        fprintf(stderr, "[gfx906_fa_amd] flat_decode: workspace of %zu bytes required, got %zu\n", need,
+                workspace_bytes);
+        return hipErrorInvalidValue;
+    }
+    FlatParams p;
+    p.q = q;
+    p.q_ts = q_token_stride;
+    p.q_hs = q_head_stride;
+    p.k = k_q8;
+    p.v = static_cast<const uint8_t *>(v_f16);
+    p.kv_len = kv_len;
+    p.q_abs = q_abs_offset;
+    p.B = batch;
+    p.Hkv = num_kv_heads;
+    p.G = G;
+    p.Sq = seq_q;
+    p.Skv = seq_kv;
+    p.P = P;
+    p.nsp = nsp;
+    p.c = scale * LOG2E;
+    p.out = out;
+    p.o_ts = out_token_stride;
+    p.o_hs = out_head_stride;
+    p.ws = static_cast<float *>(workspace);
+    const int64_t grid = (int64_t)nseg * P;
+    switch (q_dtype) {
+        case GFA_DTYPE_F32: flat_decode_kernel<GFA_DTYPE_F32><<<(unsigned)grid, 64, 0, stream>>>(p); break;
+        case GFA_DTYPE_F16: flat_decode_kernel<GFA_DTYPE_F16><<<(unsigned)grid, 64, 0, stream>>>(p); break;
+        default: flat_decode_kernel<GFA_DTYPE_BF16><<<(unsigned)grid, 64, 0, stream>>>(p); break;
+    }
+    if (P > 1) flat_combine_kernel<<<dim3(nseg, seq_q * G), 256, 0, stream>>>(p);
+    return hipGetLastError();
 }
 
 extern "C" hipError_t gfx906_fa_amd_paged_attention_tiled(

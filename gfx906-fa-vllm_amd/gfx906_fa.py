@@ -90,6 +90,9 @@ def _load():
                                                        I, I, I, I, I, I, I, I, I, F, P, I, I64, I64, P, SZ,
                                                        P, P, I, I64, I64, I64, I64, P, P]),
         "gfx906_fa_amd_pack_flat_kv": (I, [P, P, P, P, I, I, I, P]),
+        "gfx906_fa_amd_flat_decode_workspace_size": (SZ, [I, I, I, I, I]),
+        "gfx906_fa_amd_flat_decode": (I, [P, I, I64, I64, P, P, P, P, I, I, I, I, I, I, F, P, I64, I64,
+                                          P, SZ, P]),
         "gfx906_fa_amd_paged_attention_tiled": (I, [P, I, I64, I64, P, P, I, I64, I64, I64, I64, P, I64,
                                                     P, P, P, I, P, I64, I64, I, I, I, I, I, I, I, I,
                                                     F, P, I64, I64, P]),
@@ -566,7 +569,12 @@ def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: fl
     k <= q_abs_offset[b] + j (inline causal, ``kernel/fattn-q8.cuh:646-653``);
     mask fp16 [B, Sq, Skv_pad]: added to the scaled scores
     (``kernel/fattn-q8.cuh:643-644``), exclusive with q_abs_offset.  D = 128
-    only, as the reference launcher (``extension/gfx906_fa_launcher.cu:76-79``)."""
+    only, as the reference launcher (``extension/gfx906_fa_launcher.cu:76-79``).
+
+    Decode shapes (Sq * Hq / Hkv <= 16 rows per kv-head, no mask) read K and
+    V in these layouts directly, split over the keys across the device
+    (gfx906_fa_amd_flat_decode); other shapes repack K and V into the planar
+    sub-pages once per call and run the tiled prefill kernel."""
     for t, n in ((q, "q"), (k_q8, "k_q8"), (v_fp16, "v_fp16")):
         _cuda(t, n)
         _check(t.is_contiguous(), f"{n} must be contiguous")
@@ -603,11 +611,20 @@ def forward(q: torch.Tensor, k_q8: torch.Tensor, v_fp16: torch.Tensor, scale: fl
         _check(q_abs_offset.dtype == torch.int32 and q_abs_offset.dim() == 1 and q_abs_offset.shape[0] == B,
                "q_abs_offset must be 1D [B]")
         q_abs_offset = q_abs_offset.contiguous()
+    L = _load()
+    st = _stream(dev)
+    if mask is None and Sq * (Hq // Hkv) <= 16 and Skv > 0:
+        # decode shapes: the contiguous layouts read as they are, split over the keys
+        q_bshd = q.transpose(1, 2).contiguous().view(B * Sq, Hq, D)
+        ws = new_workspace(L.gfx906_fa_amd_flat_decode_workspace_size(B, Sq, Hq, Hkv, Skv), dev)
+        _ok(L.gfx906_fa_amd_flat_decode(_ptr(q_bshd), _DT[torch.float32], q_bshd.stride(0), q_bshd.stride(1),
+                                         _ptr(k_q8), _ptr(v_fp16), _ptr(sl), _ptr(q_abs_offset), B, Sq, Hq, Hkv,
+                                         Skv, D, float(scale), _ptr(out), out.stride(0), out.stride(1),
+                                         _ptr(ws), ws.numel(), st), "gfx906_fa_amd_flat_decode")
+        return out.view(B, Sq, Hq, D).transpose(1, 2).contiguous()
     skp = (max(Skv, 1) + SUBPAGE_TOKENS - 1) // SUBPAGE_TOKENS
     kp = torch.empty((B, Hkv, skp * SUBPAGE_BYTES), dtype=torch.uint8, device=dev)
     vp = torch.empty((B, Hkv, skp * 4096), dtype=torch.uint8, device=dev)
-    L = _load()
-    st = _stream(dev)
     if Skv > 0:
         _ok(L.gfx906_fa_amd_pack_flat_kv(_ptr(k_q8), _ptr(v_fp16), _ptr(kp), _ptr(vp), B * Hkv, Skv, D, st),
             "gfx906_fa_amd_pack_flat_kv")

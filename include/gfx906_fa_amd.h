@@ -382,6 +382,29 @@ hipError_t gfx906_fa_amd_paged_attention_tiled(
     int block_size, int max_query_len, float scale, float *out, int64_t out_token_stride,
     int64_t out_head_stride, hipStream_t stream);
 
+/* (7) Contiguous decode: the decode shapes of gfx906_fa_launch
+ *     (extension/gfx906_fa_launcher.cu:53-209; gfx906_fa.forward with
+ *     seq_q * num_heads / num_kv_heads <= 16 and no mask) on the reference's
+ *     own contiguous layouts, with no repacking pass: k_q8 AoS Q8_0 rows
+ *     [batch][num_kv_heads][seq_kv][136 B], v_f16 fp16 rows
+ *     [batch][num_kv_heads][seq_kv][128] (both 16-byte aligned, contiguous),
+ *     q [batch * seq_q][num_heads][128] (element strides; dtype 0/1/2),
+ *     kv_len int32 [batch] (keys each batch row sees, clamped to
+ *     [0, seq_kv]), q_abs_offset int32 [batch] or NULL (row j sees keys
+ *     k <= q_abs_offset[b] + j), out fp32 [batch * seq_q][num_heads][128]
+ *     (element strides).  Each (batch, kv-head) is split over the keys into
+ *     pieces (one single-wave workgroup each) merged by a second launch;
+ *     workspace: gfx906_fa_amd_flat_decode_workspace_size() bytes (16-byte
+ *     aligned; no initial contents).  Other shapes are refused
+ *     (hipErrorInvalidValue and a line on stderr). */
+size_t gfx906_fa_amd_flat_decode_workspace_size(int batch, int seq_q, int num_heads, int num_kv_heads,
+                                                int seq_kv);
+hipError_t gfx906_fa_amd_flat_decode(
+    const void *q, int q_dtype, int64_t q_token_stride, int64_t q_head_stride, const uint8_t *k_q8,
+    const void *v_f16, const int32_t *kv_len, const int32_t *q_abs_offset, int batch, int seq_q, int num_heads,
+    int num_kv_heads, int seq_kv, int head_size, float scale, float *out, int64_t out_token_stride,
+    int64_t out_head_stride, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Measurement helper: streams `bytes` (a multiple of 16) from the 16-byte
  * aligned device buffer `src` with non-temporal 16-byte loads and writes one
  * XOR word per wave to `out` (at least gfx906_fa_amd_stream_read_words()

@@ -96,6 +96,16 @@ def test_validation_errors_without_gpu():
     big_b = 40_000_000  # per-sequence prefix sums alone exceed 64 MiB
     assert f(None, 1, 0, 0, None, None, 0, 0, None, 0, None, None, None, 1, big_b, big_b, 48, 8, 128,
              16, 1, 16, 0.1, None, 1, 0, 0, None) == 1
+    # contiguous decode: more than 16 rows per kv-head (2 queries x 16 q-heads
+    # per kv-head) and misaligned K are refused before any launch; no work is
+    # a no-op
+    fd = L.gfx906_fa_amd_flat_decode
+    assert fd(None, 0, 0, 0, None, None, None, None, 1, 2, 16, 1, 100, 128, 0.1, None, 0, 0, None, 0,
+              None) == 1
+    assert fd(None, 0, 0, 0, ctypes.c_void_p(8), ctypes.c_void_p(16), ctypes.c_void_p(16), None, 1, 1, 8, 4, 100,
+              128, 0.1, None, 0, 0, None, 0, None) == 1
+    assert fd(None, 0, 0, 0, None, None, None, None, 1, 1, 8, 4, 0, 128, 0.1, None, 0, 0, None, 0, None) == 0
+    assert L.gfx906_fa_amd_flat_decode_workspace_size(1, 1, 8, 4, 128) == 256
     # the scratch copy helper refuses ranges past the scratch
     assert L.gfx906_fa_amd_noalloc_scratch_copy(None, 0, 16, None) == 1
     assert L.gfx906_fa_amd_noalloc_scratch_copy(ctypes.c_void_p(16), 64 << 20, 16, None) == 1
