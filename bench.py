@@ -61,6 +61,8 @@ definition instead (the line's roofline is that workload's dominant kernel):
            sequences are also timed as batches of their own (``parts``)
   cfg5     speculative verify, 6/1 heads (HBM-bound: GB/s); cfg5-48: 48/8 heads;
            cfg5-k6: 6 verify tokens (the reference's n-gram k=5), 36 rows
+  fwd-dec128k  the contiguous forward's decode (B = 1, 8/4, 131072 keys)
+  prefix72     8 x (32768 + 12) at 48/8 on 128-row prefill tiles
 """
 from __future__ import annotations
 
@@ -344,6 +346,56 @@ def _attn_fn(b, out, ws):
     return f
 
 
+def extra_workload(wl: str, dev, steps: int, warmup: int) -> dict:
+    """The rows after the hot path as workloads of their own (for kernel
+    traces and counters of their kernels):
+      fwd-dec128k  the contiguous forward, B = 1 decode, 8/4 heads, 131072
+                   keys (AoS Q8_0 K + fp16 V; flat_decode_kernel + merge)
+      prefix72     8 x (32768 + 12) at 48/8: 72 rows per kv-head on 128-row
+                   prefill tiles, split over the keys"""
+    import torch
+    import gfx906_fa
+    import gfx906_fa_workloads as W
+    base = {"metric": "Q8 paged decode HBM GB/s (% of peak); causal prefill attn TFLOP/s @32K", "n_gpus": 1,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
+    if wl == "fwd-dec128k":
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        hq, hkv, skv = 8, 4, 131072
+        q = torch.randn((1, hq, 1, 128), generator=g, device=dev)
+        k = torch.randn((1, hkv, skv, 128), generator=g, device=dev).mul_(0.1).half()
+        v = torch.randn((1, hkv, skv, 128), generator=g, device=dev).mul_(0.1).half()
+        kq = gfx906_fa.quantize_q8_0(k)
+        del k
+        ms = timed_warm(lambda: gfx906_fa.forward(q, kq, v, 1.0 / 128 ** 0.5), steps, warmup)
+        nbytes = hkv * skv * (136 + 256) + 2 * hq * 128 * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return dict(base, steps=steps, ms_per_step=round(ms, 5), dtype="f32 q, Q8_0 K, f16 V",
+                    value=round(gbs, 1), unit="GB/s",
+                    config={"workload": "fwd-dec128k: gfx906_fa.forward, B = 1, 8/4 heads, Sq 1, Skv 131072, "
+                                        "AoS Q8_0 K + fp16 V (the reference benchmark's dec_128k)",
+                            "algorithmic_bytes": nbytes, "parallelism": "single GPU"},
+                    roofline={"bound": "hbm", "kernel": "flat_decode_kernel+flat_combine_kernel",
+                              "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(ms * 1e3, 2)})
+    b = W.build_batch([32768 + 12] * 8, [12] * 8, 48, 8, seed=7, device=dev, host_values=False)
+    o = torch.empty((b.num_tokens, b.Hq, b.D), dtype=torch.float16, device=dev)
+    ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(
+        b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len, b.max_seq_len), dev)
+    ms = timed_warm(_attn_fn(b, o, ws), steps, warmup)
+    hb = b.hbm_bytes(out_bytes_per_elem=2)
+    gbs = hb / (ms * 1e-3) / 1e9
+    return dict(base, steps=steps, ms_per_step=round(ms, 5), dtype="f16", value=round(gbs, 1), unit="GB/s",
+                config={"workload": "prefix72: 8 x (32768 cached + 12 new tokens), 48/8 heads, fp16, Q8_0 K+V "
+                                    "(72 rows per kv-head: 128-row prefill tiles, split over the keys)",
+                        "algorithmic_bytes": hb, "flop": b.flops(), "parallelism": "single GPU",
+                        "pf_rows": gfx906_fa.plan_info(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len,
+                                                       b.max_seq_len)["pf_rows"]},
+                roofline={"bound": "hbm", "kernel": "attn_prefill_kernel (128-row tiles)+attn_prefill_combine_kernel",
+                          "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(ms * 1e3, 2)})
+
+
 def workload_result(wl: str, dev, steps: int, warmup: int) -> dict:
     """One attention pass of cfg3 / cfg4 / cfg5 (inputs resident in HBM),
     timed with HIP events on the launch stream: the full JSON line of
@@ -352,6 +404,9 @@ def workload_result(wl: str, dev, steps: int, warmup: int) -> dict:
 
     import gfx906_fa
     import gfx906_fa_workloads as W
+
+    if wl in ("fwd-dec128k", "prefix72"):
+        return extra_workload(wl, dev, steps, warmup)
 
     name = {"cfg5-48": "cfg5", "cfg5-k6": "cfg5k6"}.get(wl, wl)
     verify = name in ("cfg5", "cfg5k6")
@@ -433,6 +488,19 @@ def config_rows(dev, steps: int, warmup: int) -> dict:
     return rows
 
 
+def calib_copy(dev, mib: int) -> int:
+    """A plain device copy of known size (the run's last dispatch): its
+    FETCH_SIZE / WRITE_SIZE readings scale the other kernels' counters to
+    bytes."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    return n
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -447,7 +515,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (rocprof counter calibration)")
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5", "cfg5-48", "cfg5-k6"])
+    ap.add_argument("--workload", default="cfg2",
+                    choices=["cfg2", "cfg3", "cfg4", "cfg5", "cfg5-48", "cfg5-k6", "fwd-dec128k", "prefix72"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -463,7 +532,10 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.workload != "cfg2":
-        print(json.dumps(workload_result(args.workload, dev, args.steps, args.warmup)), flush=True)
+        res = workload_result(args.workload, dev, args.steps, args.warmup)
+        if args.calib_copy_mib:
+            res["calib_copy_bytes"] = calib_copy(dev, args.calib_copy_mib)
+        print(json.dumps(res), flush=True)
         return 0
 
     # ---------------- cfg2 decode -----------------------------------------
@@ -662,14 +734,7 @@ def main() -> int:
                             "reference_matrix": reference_matrix(dev)}
 
     if args.calib_copy_mib:
-        # a plain device copy of known size: its FETCH_SIZE / WRITE_SIZE
-        # readings scale the attention kernels' counters to bytes
-        n = args.calib_copy_mib << 20
-        src = torch.empty(n // 4, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        res["calib_copy_bytes"] = n
+        res["calib_copy_bytes"] = calib_copy(dev, args.calib_copy_mib)
 
     # ---------------- CPU baseline -----------------------------------------
     if not args.no_cpu:

@@ -1845,6 +1845,7 @@ constexpr int PF_SPLIT_MIN = GFA_PF_SPLIT_MIN;  // a split row tile's pieces: at
 
 // exclusive scan of v over the workgroup; *total receives the sum (a scan
 // inside each wave, then the waves' totals through tmp)
+template <int NT>
 __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     int x = v;
@@ -1858,7 +1859,7 @@ __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
     __syncthreads();
     int before = 0, tot = 0;
 #pragma unroll
-    for (int i = 0; i < PL_THREADS / 64; ++i) {
+    for (int i = 0; i < NT / 64; ++i) {
         const int t = tmp[i];
         before += i < wv ? t : 0;
         tot += t;
@@ -1888,6 +1889,7 @@ __device__ __forceinline__ int pl_ntk(const AttnParams &p, int s, int rt) {
 __device__ __forceinline__ int pl_bucket(int tiles) { return min(tiles, PL_BUCKETS - 1); }
 
 // sum of v over the workgroup (every thread receives it)
+template <int NT>
 __device__ __forceinline__ long long pl_block_sum(long long v, long long *red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -1896,11 +1898,12 @@ __device__ __forceinline__ long long pl_block_sum(long long v, long long *red) {
     __syncthreads();
     long long t = 0;
 #pragma unroll
-    for (int i = 0; i < PL_THREADS / 64; ++i) t += red[i];
+    for (int i = 0; i < NT / 64; ++i) t += red[i];
     return t;
 }
 
 // max of v over the workgroup (every thread receives it)
+template <int NT>
 __device__ __forceinline__ long long pl_block_max(long long v, long long *red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = max(v, (long long)__shfl_xor(v, off));
@@ -1909,7 +1912,7 @@ __device__ __forceinline__ long long pl_block_max(long long v, long long *red) {
     __syncthreads();
     long long t = red[0];
 #pragma unroll
-    for (int i = 1; i < PL_THREADS / 64; ++i) t = max(t, red[i]);
+    for (int i = 1; i < NT / 64; ++i) t = max(t, red[i]);
     return t;
 }
 
@@ -1917,12 +1920,13 @@ __device__ __forceinline__ long long pl_block_max(long long v, long long *red) {
 // tiles; piece c of k covers tiles [c*w/k, (c+1)*w/k).
 __device__ __forceinline__ int pl_pieces(int w, int tsplit) { return w > tsplit ? (w + tsplit - 1) / tsplit : 1; }
 
-__global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) {
+template <int NT>
+__global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
     __shared__ int s_pre[PL_MAX_SEQS + 1];  // exclusive prefix of row tiles per sequence
     __shared__ int s_bk[PL_BUCKETS];        // bucket counts, then write cursors
-    __shared__ int s_tmp[PL_THREADS / 64];
-    __shared__ long long s_red[PL_THREADS / 64];
-    __shared__ int s_w[PL_THREADS];  // key tiles of row tile i (launches of <= PL_THREADS row tiles)
+    __shared__ int s_tmp[NT / 64];
+    __shared__ long long s_red[NT / 64];
+    __shared__ int s_w[NT];  // key tiles of row tile i (launches of <= NT row tiles)
     __shared__ int s_nsplit, s_nslot;
     const int B = p.num_seqs, tid = threadIdx.x;
     int carry = 0;
@@ -1932,29 +1936,29 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     constexpr int IMG_SEQ_MAX = 1 << 20;
     long long icarry = 0;
     int ibig = 0;
-    for (int base = 0; base < B; base += PL_THREADS) {
+    for (int base = 0; base < B; base += NT) {
         const int sq = base + tid;
         const int v = sq < B ? pl_tiles(p, sq) : 0;
         int tot;
-        const int ex = pl_block_scan(v, s_tmp, &tot);
+        const int ex = pl_block_scan<NT>(v, s_tmp, &tot);
         if (sq < B) s_pre[sq] = carry + ex;
         carry += tot;
         int vt = v > 0 ? pl_ntk(p, sq, v - 1) : 0;
         ibig |= vt > IMG_SEQ_MAX;
         vt = min(vt, IMG_SEQ_MAX);
         int itot;
-        const int iex = pl_block_scan(vt, s_tmp, &itot);
+        const int iex = pl_block_scan<NT>(vt, s_tmp, &itot);
         if (p.pf_tbase != nullptr && sq < B) p.pf_tbase[sq] = (int)min(icarry + iex, (long long)INT32_MAX);
         icarry += itot;
     }
-    const bool img_big = pl_block_max(ibig, s_red) != 0;
+    const bool img_big = pl_block_max<NT>(ibig, s_red) != 0;
     if (tid == 0) {
         s_pre[B] = carry;
         s_nsplit = 0;
         s_nslot = 0;
         if (p.pf_tbase != nullptr) p.pf_tbase[B] = (int)min(icarry, (long long)INT32_MAX);
     }
-    for (int b = tid; b < PL_BUCKETS; b += PL_THREADS) s_bk[b] = 0;
+    for (int b = tid; b < PL_BUCKETS; b += NT) s_bk[b] = 0;
     __syncthreads();
     const int n = min(carry, p.pf_items_max);
     // item i -> (sequence, row tile): the last sequence whose prefix is <= i
@@ -1982,22 +1986,22 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     // tile by 10 %.  Pieces then number <= 3m and split row tiles <= 2m.
     // Past the workspace's bounds (impossible by these sums) nothing is split.
     long long wsum = 0, wmx = 0;
-    for (int i = tid; i < n; i += PL_THREADS) {
+    for (int i = tid; i < n; i += NT) {
         int sq, rt;
         locate(i, sq, rt);
         const int w = pl_ntk(p, sq, rt);
-        if (n <= PL_THREADS) s_w[i] = w;
+        if (n <= NT) s_w[i] = w;
         wsum += w;
         wmx = max(wmx, (long long)w);
     }
     // (the block reductions below order these stores before their reads)
-    auto ntk_of = [&](int i, int sq, int rt) { return n <= PL_THREADS ? s_w[i] : pl_ntk(p, sq, rt); };
-    const long long W = pl_block_sum(wsum, s_red);
-    const long long wmax = pl_block_max(wmx, s_red);  // the longest row tile
+    auto ntk_of = [&](int i, int sq, int rt) { return n <= NT ? s_w[i] : pl_ntk(p, sq, rt); };
+    const long long W = pl_block_sum<NT>(wsum, s_red);
+    const long long wmax = pl_block_max<NT>(wmx, s_red);  // the longest row tile
     long long tl = max((W * p.Hkv + p.pf_ncu - 1) / p.pf_ncu, (long long)PF_SPLIT_MIN);
     const int m = p.pf_ncu / p.Hkv;
     bool proven = false;  // the bisection's sums bound the plan: no check pass
-    if (m > 0 && n > 0 && n <= 2 * m && n <= PL_THREADS && p.pf_slots_max > 0) {
+    if (m > 0 && n > 0 && n <= 2 * m && n <= NT && p.pf_slots_max > 0) {
         int wt = 0;  // thread t holds row tile t's key tiles
         if (tid < n) wt = s_w[tid];
         const int rounds0 = (n + m - 1) / m;       // unsplit, all row tiles alike
@@ -2009,7 +2013,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         long long hi = max(lo, (W + (cap - n) - 1) / (cap - n));
         while (lo < hi) {
             const long long mid = (lo + hi) >> 1;
-            const long long P = pl_block_sum(tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0, s_red);
+            const long long P = pl_block_sum<NT>(tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0, s_red);
             if (P <= cap) hi = mid;
             else lo = mid + 1;
         }
@@ -2021,7 +2025,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
     int tsplit = (p.pf_slots_max > 0 && tl < wmax) ? (int)tl : INT32_MAX;  // else nothing is cut
     if (tsplit < INT32_MAX && !proven) {
         long long ex = 0, sl = 0, ns = 0;
-        for (int i = tid; i < n; i += PL_THREADS) {
+        for (int i = tid; i < n; i += NT) {
             int sq, rt;
             locate(i, sq, rt);
             const int k = pl_pieces(ntk_of(i, sq, rt), tsplit);
@@ -2031,12 +2035,12 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
                 ns += 1;
             }
         }
-        ex = pl_block_sum(ex, s_red);
-        sl = pl_block_sum(sl, s_red);
-        ns = pl_block_sum(ns, s_red);
+        ex = pl_block_sum<NT>(ex, s_red);
+        sl = pl_block_sum<NT>(sl, s_red);
+        ns = pl_block_sum<NT>(ns, s_red);
         if (n + ex > p.pf_grid_items || sl > p.pf_slots_max || ns > p.pf_split_max) tsplit = INT32_MAX;
     }
-    for (int i = tid; i < n; i += PL_THREADS) {
+    for (int i = tid; i < n; i += NT) {
         int sq, rt;
         locate(i, sq, rt);
         const int w = ntk_of(i, sq, rt);
@@ -2050,18 +2054,18 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         }
     }
     __syncthreads();
-    // write cursors in descending bucket order: thread t owns buckets
-    // B-1-4t .. B-4-4t
+    // write cursors in descending bucket order: thread t owns the PER
+    // buckets B-1-PER*t .. B-PER-PER*t
     int total;
     {
-        constexpr int PER = PL_BUCKETS / PL_THREADS;
+        constexpr int PER = PL_BUCKETS / NT;
         int c[PER], loc = 0;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             c[k] = s_bk[PL_BUCKETS - 1 - (PER * tid + k)];
             loc += c[k];
         }
-        int run = pl_block_scan(loc, s_tmp, &total);
+        int run = pl_block_scan<NT>(loc, s_tmp, &total);
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             s_bk[PL_BUCKETS - 1 - (PER * tid + k)] = run;
@@ -2069,7 +2073,7 @@ __global__ __launch_bounds__(PL_THREADS) void prefill_plan_kernel(AttnParams p) 
         }
     }
     __syncthreads();
-    for (int i = tid; i < n; i += PL_THREADS) {
+    for (int i = tid; i < n; i += NT) {
         int sq, rt;
         locate(i, sq, rt);
         const int w = ntk_of(i, sq, rt);
@@ -2457,13 +2461,17 @@ __global__ __launch_bounds__(64) void flat_decode_kernel(FlatParams p) {
     }
 }
 
-// Merges the P pieces of each (segment, row): grid (B * Hkv, Sq * G), 256
-// threads.  Thread t owns d-chunk t % 32 (4 d) and pieces t / 32, t / 32 + 8,
-// ... (one-pass online merge, four pieces' loads in flight); the 8 partial
-// states per d-chunk are merged through LDS.
-__global__ __launch_bounds__(256) void flat_combine_kernel(FlatParams p) {
-    __shared__ float sm_m[8], sm_l[8];
-    __shared__ float4_t sm_o[8][32];
+// Merges the P pieces of each (segment, row): grid (B * Hkv, Sq * G), 1024
+// threads.  Thread t owns d-chunk t % 32 (4 d) and pieces t / 32, t / 32 +
+// 32, ... (one-pass online merge, eight pieces' loads in flight: 256 pieces
+// per round trip); the 32 partial states per d-chunk are merged through
+// LDS.  (A segment is often cut into hundreds of pieces for few rows, so the
+// merge is latency-bound: with 256 threads and four loads in flight, 512
+// pieces took 14 us.)
+constexpr int FC_THREADS = 1024, FC_GROUPS = FC_THREADS / 32, FC_U = 8;
+__global__ __launch_bounds__(FC_THREADS) void flat_combine_kernel(FlatParams p) {
+    __shared__ float sm_m[FC_GROUPS], sm_l[FC_GROUPS];
+    __shared__ float4_t sm_o[FC_GROUPS][32];
     const int seg = blockIdx.x, r = blockIdx.y;
     const int nrows = p.Sq * p.G;
     const int t = threadIdx.x, grp = t >> 5, d0 = 4 * (t & 31);
@@ -2471,18 +2479,18 @@ __global__ __launch_bounds__(256) void flat_combine_kernel(FlatParams p) {
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
     const float *base = p.ws + ((int64_t)seg * p.P * nrows + r) * FD_ROW;
     const int64_t pstep = (int64_t)nrows * FD_ROW;  // piece k -> k + 1
-    for (int k0 = grp; k0 < p.P; k0 += 32) {
-        float2_t ml[4];
-        float4_t oc[4];
+    for (int k0 = grp; k0 < p.P; k0 += FC_GROUPS * FC_U) {
+        float2_t ml[FC_U];
+        float4_t oc[FC_U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int k = k0 + 8 * u;
+        for (int u = 0; u < FC_U; ++u) {
+            const int k = k0 + FC_GROUPS * u;
             const float *row = base + k * pstep;
             ml[u] = k < p.P ? *reinterpret_cast<const float2_t *>(row) : float2_t{-INFINITY, 0.f};
             oc[u] = k < p.P ? *reinterpret_cast<const float4_t *>(row + 4 + d0) : float4_t{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < FC_U; ++u) {
             const float mc = ml[u][0];
             if (mc > -INFINITY) {
                 const float mn = fmaxf(M, mc);
@@ -2503,12 +2511,12 @@ __global__ __launch_bounds__(256) void flat_combine_kernel(FlatParams p) {
     if (grp != 0) return;
     float mx = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, sm_m[k]);
+    for (int k = 0; k < FC_GROUPS; ++k) mx = fmaxf(mx, sm_m[k]);
     const float ms = mx == -INFINITY ? 0.0f : mx;
     float l = 0.f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < FC_GROUPS; ++k) {
         const float wk = sm_m[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm_m[k] - ms);
         l = fmaf(sm_l[k], wk, l);
         o += sm_o[k][t & 31] * wk;
@@ -2762,7 +2770,13 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
     AttnParams p = p0;
     p.dec_rows_lo = 0;
     p.dec_rows_max = pl.dec_rows_max;
-    if (pl.need_prefill && p.pf_seq) prefill_plan_kernel<<<1, PL_THREADS, 0, stream>>>(p);
+    if (pl.need_prefill && p.pf_seq) {
+        // one wave for small batches: its scans and reductions need no
+        // barriers across 16 waves (8 x (32768 + 12) at 48/8: 18.6 us with
+        // 1024 threads)
+        if (num_seqs <= 64 && pl.pf_items_max <= 64) prefill_plan_kernel<64><<<1, 64, 0, stream>>>(p);
+        else prefill_plan_kernel<PL_THREADS><<<1, PL_THREADS, 0, stream>>>(p);
+    }
     for (int k = 0; k < pl.ndc; ++k) {
         const DecClass &c = pl.dc[k];
         AttnParams pd = p;
@@ -3236,7 +3250,7 @@ extern "C" hipError_t gfx906_fa_amd_flat_decode(
         case GFA_DTYPE_F16: flat_decode_kernel<GFA_DTYPE_F16><<<(unsigned)grid, 64, 0, stream>>>(p); break;
         default: flat_decode_kernel<GFA_DTYPE_BF16><<<(unsigned)grid, 64, 0, stream>>>(p); break;
     }
-    if (P > 1) flat_combine_kernel<<<dim3(nseg, seq_q * G), 256, 0, stream>>>(p);
+    if (P > 1) flat_combine_kernel<<<dim3(nseg, seq_q * G), FC_THREADS, 0, stream>>>(p);
     return hipGetLastError();
 }
 
