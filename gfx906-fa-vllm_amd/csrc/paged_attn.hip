@@ -2667,9 +2667,10 @@ void plan_finish(Plan &pl, int num_seqs, int64_t num_tokens, int G, int num_kv_h
     pl.off_items = off;
     // work list: a 256-byte header (item count, split row tile count), the
     // five item arrays, the split list, then the partials of the split pieces
-    // (slots of PF_ROWS rows, which also hold the PF_ROWS / 2 of KS = 2 tiles)
+    // (slots of the call's tile rows)
     pl.off_split = pl.off_items + 256 + align256((size_t)5 * grid_items * sizeof(int));
-    const size_t prow = (size_t)pl.pf_slots_max * num_kv_heads * PF_ROWS;
+    // partial slots of the call's tile rows (a bound over every call: PF_ROWS)
+    const size_t prow = (size_t)pl.pf_slots_max * num_kv_heads * (force_pf ? PF_ROWS : pl.pf_rows);
     pl.off_pml = pl.off_split + align256((size_t)4 * pl.pf_split_max * sizeof(int));
     pl.off_po = pl.off_pml + align256(prow * 2 * sizeof(float));
     // the per-sequence first image tile, then (optional) the images: every

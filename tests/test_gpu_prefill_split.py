@@ -155,13 +155,17 @@ def test_split_prefill_q_abs_offset():
     assert_close(to_np_f32(out), ref)
 
 
-def test_split_prefill_graph_replay():
+@pytest.mark.parametrize("nq", [60, 12])
+def test_split_prefill_graph_replay(nq):
     """One chunked-prefill launch captured in a HIP graph, replayed with new
     sequence lengths (so a different split) and query values; every replay
-    equals the eager call bit for bit, the last one the oracle."""
+    equals the eager call bit for bit, the last one the oracle.  60 tokens at
+    48/8 are 360 rows per kv-head (256-row tiles), 12 tokens 72 rows (128-row
+    key-interleaved tiles)."""
     need_gpu()
-    announce("prefill split graph replay")
-    B, nq, Hq, Hkv, bs, max_blocks = 2, 60, 48, 8, 16, 640
+    announce(f"prefill split graph replay nq={nq}")
+    B, Hq, Hkv, bs, max_blocks = 2, 48, 8, 16, 640
+    assert gfx906_fa.plan_info(B, B * nq, Hq, Hkv, nq, max_blocks * bs)["pf_rows"] == (256 if nq == 60 else 128)
     NB = B * max_blocks
     T = B * nq
     rng = np.random.default_rng(93)

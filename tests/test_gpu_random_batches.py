@@ -48,6 +48,37 @@ def test_random_batch_matches_oracle(seed):
     assert_close(to_np_f32(out), batch_oracle(b))
 
 
+def _draw_rows128(seed):
+    """A batch whose prefill chunks have 65-128 rows per kv-head (the longest
+    at least 65), beside decode and verify sequences: the 128-row
+    key-interleaved prefill tiles, split or whole."""
+    rng = np.random.default_rng(3000 + seed)
+    hq, hkv = HEADS[seed % len(HEADS)]
+    G = hq // hkv
+    nseq = int(rng.integers(1, 41))
+    lo, hi = 64 // G + 1, 128 // G
+    kind = rng.choice(3, size=nseq, p=[0.5, 0.2, 0.3])
+    ql = np.where(kind == 0, 1, np.where(kind == 1, rng.integers(2, max(3, lo), nseq), rng.integers(lo, hi + 1, nseq)))
+    ql[int(rng.integers(nseq))] = int(rng.integers(lo, hi + 1))
+    ctx = rng.integers(0, 20000, nseq)
+    sl = [int(q + c) for q, c in zip(ql, ctx)]
+    return sl, [int(q) for q in ql], hq, hkv, int(rng.choice([16, 32, 64])), "bf16" if seed % 2 else "f16"
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batch_rows128_matches_oracle(seed):
+    need_gpu()
+    sl, ql, hq, hkv, bs, dt = _draw_rows128(seed)
+    announce(f"random rows128 batch seed={seed} B={len(sl)} heads={hq}/{hkv} bs={bs} {dt} "
+             f"max_q={max(ql)} max_k={max(sl)}")
+    b = W.build_batch(sl, ql, hq, hkv, block_size=bs, dtype=dt, seed=4000 + seed)
+    info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, hq, hkv, b.max_query_len, b.max_seq_len)
+    assert info["pf_rows"] == 128, info
+    out = W.attention(b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(to_np_f32(out), batch_oracle(b))
+
+
 PROMPT_HEADS = [(8, 1), (64, 4), (24, 3), (48, 8), (32, 8), (16, 2)]
 
 

@@ -128,3 +128,24 @@ def test_noalloc_prompt_with_tile_images():
     assert torch.equal(out, ref)
     hdr = _scratch_header(b)
     assert hdr[2] == 1 and hdr[3] > 0, hdr  # the images were written in the scratch
+
+
+def test_noalloc_rows128_bitidentical():
+    """Chunks of 12 tokens at 48/8 (72 rows per kv-head: the 128-row
+    key-interleaved prefill tiles), on a long prefix and then a shorter one:
+    the noalloc entry takes the workspace entry's plan where its split
+    partials fit the scratch, so the output is the same bits."""
+    need_gpu()
+    first = W.build_batch([20000 + 12, 900 + 12], [12, 12], 48, 8, seed=78)
+    second = W.build_batch([3000 + 12], [12], 48, 8, seed=79)
+    for name, b in (("2 chunks of 12 on 20K / 900, 48/8", first), ("1 chunk of 12 on 3K", second)):
+        announce(f"noalloc rows128 {name}")
+        info = gfx906_fa.plan_info(b.num_seqs, b.num_tokens, 48, 8, b.max_query_len, b.max_seq_len)
+        assert info["pf_rows"] == 128 and info["img_offset"] <= 64 << 20, info
+        ref = _with_workspace(b, torch.float32)
+        out = torch.full_like(ref, 3.0)
+        _noalloc(b, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), name
+        if b is first:
+            assert _scratch_header(b)[1] > 0  # split over the keys, as with a workspace
