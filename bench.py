@@ -377,7 +377,8 @@ def extra_workload(wl: str, dev, steps: int, warmup: int) -> dict:
                             "algorithmic_bytes": nbytes, "parallelism": "single GPU"},
                     roofline={"bound": "hbm", "kernel": "flat_decode_kernel+flat_combine_kernel",
                               "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(ms * 1e3, 2)})
+                              "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _traffic("flat_decode_fwd128k"),
+                              "avg_us": round(ms * 1e3, 2)})
     b = W.build_batch([32768 + 12] * 8, [12] * 8, 48, 8, seed=7, device=dev, host_values=False)
     o = torch.empty((b.num_tokens, b.Hq, b.D), dtype=torch.float16, device=dev)
     ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(
@@ -393,7 +394,8 @@ def extra_workload(wl: str, dev, steps: int, warmup: int) -> dict:
                                                        b.max_seq_len)["pf_rows"]},
                 roofline={"bound": "hbm", "kernel": "attn_prefill_kernel (128-row tiles)+attn_prefill_combine_kernel",
                           "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(ms * 1e3, 2)})
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": _traffic("attn_prefill_prefix72"),
+                          "avg_us": round(ms * 1e3, 2)})
 
 
 def workload_result(wl: str, dev, steps: int, warmup: int) -> dict:
