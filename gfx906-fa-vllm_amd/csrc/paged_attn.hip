@@ -227,6 +227,11 @@ __device__ __forceinline__ void acc_init(WaveAcc<NRG> &a) {
 // (d_v <= 65504/127) and for bf16 V with |v| < 1.3e5.
 constexpr float LAZY_TAU = 6.0f;
 
+// Max of three through fmaxf (the compiler forms v_max3_f32).  Not inline
+// assembly: the compiler's wait states between an MFMA and a VALU read of
+// its result do not cover instructions inside asm statements.
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
 __device__ __forceinline__ float4_t mfma16k16(half4_t a, half4_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
@@ -265,9 +270,13 @@ __device__ __forceinline__ void attend_subpage(WaveAcc<NRG> &acc, const SubPage 
                 sv[i] = (key < kv_end && key <= lim[rg]) ? sv[i] : -INFINITY;
             }
         }
-        float mt = xrow_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
-        const bool need = mt > acc.m[rg] + LAZY_TAU;
-        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after warm-up
+        // The lane's max over its 4 keys; a row's max is the largest of its
+        // four lanes' (i16 + 16 g), so no lane above m + LAZY_TAU means no row
+        // is, and the cross-lane step runs only when some row may rescale.
+        const float ml = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])) * c;
+        if (__builtin_amdgcn_ballot_w64(ml > acc.m[rg] + LAZY_TAU)) {  // wave-uniform, rare after warm-up
+            const float mt = xrow_max(ml);
+            const bool need = mt > acc.m[rg] + LAZY_TAU;
             const float mn = need ? mt : acc.m[rg];
             // 0 when m was -inf (nothing accumulated yet); 1 for rows that keep m
             const float alpha = need ? __builtin_amdgcn_exp2f(acc.m[rg] - mn) : 1.0f;
@@ -1167,6 +1176,21 @@ __device__ __forceinline__ float16v_t mfma32(half8_t a, half8_t b, float16v_t c)
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Max over the 32 values of two S accumulators as a tree of depth 4 (a
+// running fmaxf chain is 16 dependent steps deep).
+__device__ __forceinline__ float tile_max32(const float16v_t &x, const float16v_t &y) {
+    float b[11];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) b[i] = max3f(x[3 * i], x[3 * i + 1], x[3 * i + 2]);
+    b[5] = max3f(x[15], y[0], y[1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[6 + i] = max3f(y[2 + 3 * i], y[3 + 3 * i], y[4 + 3 * i]);
+    b[10] = y[14];
+    const float c0 = max3f(b[0], b[1], b[2]), c1 = max3f(b[3], b[4], b[5]);
+    const float c2 = max3f(b[6], b[7], b[8]), c3 = max3f(b[9], b[10], y[15]);
+    return max3f(max3f(c0, c1, c2), c3, c3);
+}
+
 // Raw bytes of one half (hf = 0, 1) of a sub-page as a lane holds them:
 // the Q8_0 blocks 2hf and 2hf+1 of K and of V.
 //   K: token t = l%16, group g = l/16: k = ints of d = 8g + 32b + (0..7),
@@ -1594,6 +1618,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     // core directly.  has_m: a visible key has been seen (m valid).
     float m_use = 0.0f, l_run = 0.0f;
     bool has_m = false;
+    bool all_m = false;  // wave-uniform: every lane's has_m
 
     // lane-constant LDS offsets of the MFMA operands
     const int kread = (lane & 31) * PF_KPITCH + 16 * hb;  // + 32*st*KPITCH + 32*kk
@@ -1664,28 +1689,30 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
                     sacc[st][e] = key <= lim ? sacc[st][e] : -INFINITY;
                 }
         }
-        float mx = sacc[0][0];
-#pragma unroll
-        for (int st = 0; st < PF_NST; ++st)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
-        {
+        // The lane's own max over its 32 keys, as a tree of depth 4.  A row's
+        // max is the larger of its two lanes', so
+        // "every lane <= LAZY_TAU once every row has m" is exactly the case in
+        // which the rescale below would change nothing: that test needs no
+        // cross-lane step.
+        float mx = tile_max32(sacc[0], sacc[1]);
+        if (!all_m || __builtin_amdgcn_ballot_w64(mx > LAZY_TAU)) {  // wave-uniform, rare after the first tile
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
             mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        // lazy rescale: move m only when the tile max exceeds it by > LAZY_TAU
-        // (or on the first visible key of the row)
-        const bool need = has_m ? mx > LAZY_TAU : mx > -INFINITY;
-        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after the first tile
-            const float delta = need ? mx : 0.0f;
-            const float alpha = (need && has_m) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
-            m_use += delta;
-            has_m = has_m || need;
-            l_run *= alpha;
+            // lazy rescale: move m only when the tile max exceeds it by > LAZY_TAU
+            // (or on the first visible key of the row)
+            const bool need = has_m ? mx > LAZY_TAU : mx > -INFINITY;
+            if (__builtin_amdgcn_ballot_w64(need)) {
+                const float delta = need ? mx : 0.0f;
+                const float alpha = (need && has_m) ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+                m_use += delta;
+                has_m = has_m || need;
+                l_run *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+                for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
 #pragma unroll
-            for (int st = 0; st < PF_NST; ++st) sacc[st] -= delta;
+                for (int st = 0; st < PF_NST; ++st) sacc[st] -= delta;
+            }
+            all_m = __builtin_amdgcn_ballot_w64(!has_m) == 0;
         }
         // Row sum of the fp16-rounded p with v_dot2 (the same values the PV
         // MFMAs consume).
@@ -2405,9 +2432,12 @@ __global__ __launch_bounds__(64) void flat_decode_kernel(FlatParams p) {
                 sv[i] = (key < kvl && key <= lim) ? sv[i] : -INFINITY;
             }
         }
-        const float mt = xrow_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))) * c;
-        const bool need = mt > m + LAZY_TAU;
-        if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform, rare after warm-up
+        // lane-local test first; the row's max (over lanes i16 + 16 g) only
+        // when some lane may rescale
+        const float ml = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])) * c;
+        if (__builtin_amdgcn_ballot_w64(ml > m + LAZY_TAU)) {  // wave-uniform, rare after warm-up
+            const float mt = xrow_max(ml);
+            const bool need = mt > m + LAZY_TAU;
             const float mn = need ? mt : m;
             const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
             m = mn;
