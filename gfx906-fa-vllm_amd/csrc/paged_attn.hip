@@ -1870,6 +1870,39 @@ constexpr int PF_SPLIT_MIN = GFA_PF_SPLIT_MIN;  // a split row tile's pieces: at
 #define GFA_PFC_WGS_PER_CU 4  // split-merge workgroups per CU (more loads in flight)
 #endif
 
+// The plan's workgroup-wide ordering point.  On one wave (NT = 64) it needs
+// no barrier: a wave's LDS instructions complete in the order it issues
+// them, and the wave-scope fence keeps the compiler from moving LDS accesses
+// across it.  (A workgroup barrier would also wait for the wave's global
+// stores to complete, which the plan never needs.)
+template <int NT>
+__device__ __forceinline__ void pl_sync() {
+    if constexpr (NT == 64) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    } else {
+        __syncthreads();
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// sum over the wave, every lane receives it: butterflies within each 16-lane
+// DPP row, then across the four rows with the permlane swaps
+__device__ __forceinline__ int pl_wave_sum32(int v) {
+    v += dpp_i32<DPP_QUAD_XOR1>(v);
+    v += dpp_i32<DPP_QUAD_XOR2>(v);
+    v += dpp_i32<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_i32<DPP_ROW_MIRROR>(v);
+    const auto a = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = (int)(a[0] + a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return (int)(b[0] + b[1]);
+}
+
 // exclusive scan of v over the workgroup; *total receives the sum (a scan
 // inside each wave, then the waves' totals through tmp)
 template <int NT>
@@ -1880,6 +1913,10 @@ __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
     for (int off = 1; off < 64; off <<= 1) {
         const int y = __shfl_up(x, off);
         if (lane >= off) x += y;
+    }
+    if constexpr (NT == 64) {
+        *total = __builtin_amdgcn_readlane(x, 63);
+        return x - v;
     }
     __syncthreads();  // tmp[] of a previous call has been read
     if (lane == 63) tmp[wv] = x;
@@ -1895,21 +1932,41 @@ __device__ __forceinline__ int pl_block_scan(int v, int *tmp, int *total) {
     return before + x - v;
 }
 
-__device__ __forceinline__ int pl_tiles(const AttnParams &p, int s) {
-    const int nq = p.qsl[s + 1] - p.qsl[s];
-    const int nrows = nq * p.G;
-    return (nq > 0 && nrows > p.dec_rows_max) ? (nrows + p.pf_rows - 1) / p.pf_rows : 0;
+// floor(a / b) for a >= 0, b >= 1.  Below 2^22 from the float quotient,
+// which is then within 1 of it, and one correction each way (the compiler's
+// integer division is a long instruction sequence).
+__device__ __forceinline__ int pl_div(int a, int b) {
+    if (a >= (1 << 22)) return a / b;
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+    const int r = a - q * b;
+    q += r < 0 ? -1 : (r >= b ? 1 : 0);
+    return q;
 }
 
-// 64-key tiles row tile rt of sequence s attends (the prefill kernel's ntk_all)
-__device__ __forceinline__ int pl_ntk(const AttnParams &p, int s, int rt) {
-    const int q0 = p.qsl[s];
-    const int nq = p.qsl[s + 1] - q0;
-    const int nrows = nq * p.G;
-    const int sl = p.seq_lens[s];
-    const int qa = p.q_abs ? p.q_abs[s] : sl - nq;
-    const int jlast = (min(p.pf_rows * (rt + 1), nrows) - 1) / p.G;
-    const int kv_end = p.causal ? min(sl, max(qa + jlast + 1, 0)) : sl;
+// A sequence's scalars as the plan reads them.
+struct PlSeq {
+    int nq, sl, qa;
+};
+
+__device__ __forceinline__ PlSeq pl_seq(const AttnParams &p, int s) {
+    PlSeq q;
+    q.nq = p.qsl[s + 1] - p.qsl[s];
+    q.sl = p.seq_lens[s];
+    q.qa = p.q_abs ? p.q_abs[s] : q.sl - q.nq;
+    return q;
+}
+
+// prefill row tiles of a sequence (0 for decode sequences)
+__device__ __forceinline__ int pl_tiles(const AttnParams &p, const PlSeq &q) {
+    const int nrows = q.nq * p.G;
+    return (q.nq > 0 && nrows > p.dec_rows_max) ? pl_div(nrows + p.pf_rows - 1, p.pf_rows) : 0;
+}
+
+// 64-key tiles row tile rt of a sequence attends (the prefill kernel's ntk_all)
+__device__ __forceinline__ int pl_ntk(const AttnParams &p, const PlSeq &q, int rt) {
+    const int nrows = q.nq * p.G;
+    const int jlast = pl_div(min(p.pf_rows * (rt + 1), nrows) - 1, p.G);
+    const int kv_end = p.causal ? min(q.sl, max(q.qa + jlast + 1, 0)) : q.sl;
     return (kv_end + PF_TK - 1) / PF_TK;
 }
 
@@ -1920,6 +1977,7 @@ template <int NT>
 __device__ __forceinline__ long long pl_block_sum(long long v, long long *red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if constexpr (NT == 64) return uniform64(v);  // (in scalar registers: the plan's control flow is uniform)
     __syncthreads();  // red[] of a previous call has been read
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -1934,6 +1992,7 @@ template <int NT>
 __device__ __forceinline__ long long pl_block_max(long long v, long long *red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = max(v, (long long)__shfl_xor(v, off));
+    if constexpr (NT == 64) return uniform64(v);
     __syncthreads();  // red[] of a previous call has been read
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -1945,7 +2004,7 @@ __device__ __forceinline__ long long pl_block_max(long long v, long long *red) {
 
 // Pieces row tile of w key tiles is cut into when pieces hold at most tsplit
 // tiles; piece c of k covers tiles [c*w/k, (c+1)*w/k).
-__device__ __forceinline__ int pl_pieces(int w, int tsplit) { return w > tsplit ? (w + tsplit - 1) / tsplit : 1; }
+__device__ __forceinline__ int pl_pieces(int w, int tsplit) { return w > tsplit ? pl_div(w + tsplit - 1, tsplit) : 1; }
 
 template <int NT>
 __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
@@ -1954,6 +2013,7 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
     __shared__ int s_tmp[NT / 64];
     __shared__ long long s_red[NT / 64];
     __shared__ int s_w[NT];  // key tiles of row tile i (launches of <= NT row tiles)
+    __shared__ PlSeq s_seq[NT];  // the sequences' scalars (launches of <= NT sequences)
     __shared__ int s_nsplit, s_nslot;
     const int B = p.num_seqs, tid = threadIdx.x;
     int carry = 0;
@@ -1965,12 +2025,15 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
     int ibig = 0;
     for (int base = 0; base < B; base += NT) {
         const int sq = base + tid;
-        const int v = sq < B ? pl_tiles(p, sq) : 0;
+        PlSeq qs = {0, 0, 0};
+        if (sq < B) qs = pl_seq(p, sq);  // one round of loads
+        if (B <= NT) s_seq[tid] = qs;
+        const int v = sq < B ? pl_tiles(p, qs) : 0;
         int tot;
         const int ex = pl_block_scan<NT>(v, s_tmp, &tot);
         if (sq < B) s_pre[sq] = carry + ex;
         carry += tot;
-        int vt = v > 0 ? pl_ntk(p, sq, v - 1) : 0;
+        int vt = v > 0 ? pl_ntk(p, qs, v - 1) : 0;
         ibig |= vt > IMG_SEQ_MAX;
         vt = min(vt, IMG_SEQ_MAX);
         int itot;
@@ -1985,9 +2048,9 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
         s_nslot = 0;
         if (p.pf_tbase != nullptr) p.pf_tbase[B] = (int)min(icarry, (long long)INT32_MAX);
     }
-    for (int b = tid; b < PL_BUCKETS; b += NT) s_bk[b] = 0;
-    __syncthreads();
+    pl_sync<NT>();
     const int n = min(carry, p.pf_items_max);
+    auto seq_of = [&](int sq) { return B <= NT ? s_seq[sq] : pl_seq(p, sq); };
     // item i -> (sequence, row tile): the last sequence whose prefix is <= i
     auto locate = [&](int i, int &sq, int &rt) {
         int lo = 0, hi = B - 1;
@@ -2016,13 +2079,13 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
     for (int i = tid; i < n; i += NT) {
         int sq, rt;
         locate(i, sq, rt);
-        const int w = pl_ntk(p, sq, rt);
+        const int w = pl_ntk(p, seq_of(sq), rt);
         if (n <= NT) s_w[i] = w;
         wsum += w;
         wmx = max(wmx, (long long)w);
     }
     // (the block reductions below order these stores before their reads)
-    auto ntk_of = [&](int i, int sq, int rt) { return n <= NT ? s_w[i] : pl_ntk(p, sq, rt); };
+    auto ntk_of = [&](int i, int sq, int rt) { return n <= NT ? s_w[i] : pl_ntk(p, seq_of(sq), rt); };
     const long long W = pl_block_sum<NT>(wsum, s_red);
     const long long wmax = pl_block_max<NT>(wmx, s_red);  // the longest row tile
     long long tl = max((W * p.Hkv + p.pf_ncu - 1) / p.pf_ncu, (long long)PF_SPLIT_MIN);
@@ -2040,7 +2103,13 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
         long long hi = max(lo, (W + (cap - n) - 1) / (cap - n));
         while (lo < hi) {
             const long long mid = (lo + hi) >> 1;
-            const long long P = pl_block_sum<NT>(tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0, s_red);
+            long long P;
+            if constexpr (NT == 64) {  // 32-bit DPP sum; counts above 2^24 only need to exceed cap
+                const int k = tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0;
+                P = __builtin_amdgcn_readfirstlane(pl_wave_sum32(min(k, 1 << 24)));
+            } else {
+                P = pl_block_sum<NT>(tid < n ? pl_pieces(wt, (int)min(mid, (long long)INT32_MAX)) : 0, s_red);
+            }
             if (P <= cap) hi = mid;
             else lo = mid + 1;
         }
@@ -2067,6 +2136,11 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
         ns = pl_block_sum<NT>(ns, s_red);
         if (n + ex > p.pf_grid_items || sl > p.pf_slots_max || ns > p.pf_split_max) tsplit = INT32_MAX;
     }
+    // buckets that can hold an item: an unsplit row tile has at most
+    // min(wmax, tsplit) key tiles, and so has a piece of a split one
+    const int nb = (int)min(min(wmax, (long long)tsplit), (long long)PL_BUCKETS - 1) + 1;
+    for (int b = tid; b < nb; b += NT) s_bk[b] = 0;
+    pl_sync<NT>();
     for (int i = tid; i < n; i += NT) {
         int sq, rt;
         locate(i, sq, rt);
@@ -2075,31 +2149,33 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
         if (k == 1) {
             atomicAdd(&s_bk[pl_bucket(w)], 1);
         } else {  // w % k pieces of w / k + 1 tiles, the others of w / k
-            const int big = w % k;
-            if (big) atomicAdd(&s_bk[pl_bucket(w / k + 1)], big);
-            atomicAdd(&s_bk[pl_bucket(w / k)], k - big);
+            const int q = pl_div(w, k), big = w - q * k;
+            if (big) atomicAdd(&s_bk[pl_bucket(q + 1)], big);
+            atomicAdd(&s_bk[pl_bucket(q)], k - big);
         }
     }
-    __syncthreads();
-    // write cursors in descending bucket order: thread t owns the PER
-    // buckets B-1-PER*t .. B-PER-PER*t
+    pl_sync<NT>();
+    // write cursors in descending bucket order: thread t owns the per
+    // buckets nb-1-per*t .. nb-per-per*t (those >= 0)
     int total;
     {
-        constexpr int PER = PL_BUCKETS / NT;
-        int c[PER], loc = 0;
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            c[k] = s_bk[PL_BUCKETS - 1 - (PER * tid + k)];
-            loc += c[k];
+        const int per = (nb + NT - 1) / NT;
+        int loc = 0;
+        for (int k = 0; k < per; ++k) {
+            const int b = nb - 1 - (per * tid + k);
+            if (b >= 0) loc += s_bk[b];
         }
         int run = pl_block_scan<NT>(loc, s_tmp, &total);
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            s_bk[PL_BUCKETS - 1 - (PER * tid + k)] = run;
-            run += c[k];
+        for (int k = 0; k < per; ++k) {
+            const int b = nb - 1 - (per * tid + k);
+            if (b >= 0) {
+                const int c = s_bk[b];
+                s_bk[b] = run;
+                run += c;
+            }
         }
     }
-    __syncthreads();
+    pl_sync<NT>();
     for (int i = tid; i < n; i += NT) {
         int sq, rt;
         locate(i, sq, rt);
@@ -2114,8 +2190,15 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
             e[2] = slot0;
             e[3] = k;
         }
+        // piece c: tiles [c w / k, (c + 1) w / k), stepped without a division:
+        // (c + 1) w = (a + q) k + (rem + rw) for a = c w / k, rem = c w % k
+        const int q = pl_div(w, k), rw = w - q * k;
+        int b = 0, rem = 0;
         for (int c = 0; c < k; ++c) {
-            const int a = (int)((long long)c * w / k), b = (int)((long long)(c + 1) * w / k);
+            const int a = b;
+            rem += rw;
+            b = a + q + (rem >= k ? 1 : 0);
+            rem -= rem >= k ? k : 0;
             const int pos = atomicAdd(&s_bk[pl_bucket(b - a)], 1);
             p.pf_seq[pos] = sq;
             p.pf_rt[pos] = rt;
@@ -2124,7 +2207,7 @@ __global__ __launch_bounds__(NT) void prefill_plan_kernel(AttnParams p) {
             p.pf_slot[pos] = k > 1 ? slot0 + c : -1;
         }
     }
-    __syncthreads();
+    pl_sync<NT>();
     if (tid == 0) {
         p.pf_count[0] = total;
         p.pf_count[1] = s_nsplit;
