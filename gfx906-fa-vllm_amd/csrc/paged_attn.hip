@@ -2574,20 +2574,26 @@ __global__ __launch_bounds__(64) void flat_decode_kernel(FlatParams p) {
     }
 }
 
-// Merges the P pieces of each (segment, row): grid (B * Hkv, Sq * G), 1024
-// threads.  Thread t owns d-chunk t % 32 (4 d) and pieces t / 32, t / 32 +
-// 32, ... (one-pass online merge, eight pieces' loads in flight: 256 pieces
-// per round trip); the 32 partial states per d-chunk are merged through
+// Merges the P pieces of each (segment, row): grid (B * Hkv, Sq * G, FC_DS),
+// 1024 threads; workgroup z takes 128 / FC_DS of the d.  Thread t owns the
+// 4-d chunk t % FC_DCH of them and pieces t / FC_DCH + FC_GROUPS k (one-pass
+// online merge, eight pieces' loads in flight: 8 FC_GROUPS pieces per round
+// trip); the FC_GROUPS partial states per chunk then merge in a tree through
 // LDS.  (A segment is often cut into hundreds of pieces for few rows, so the
 // merge is latency-bound: with 256 threads and four loads in flight, 512
-// pieces took 14 us.)
-constexpr int FC_THREADS = 1024, FC_GROUPS = FC_THREADS / 32, FC_U = 8;
+// pieces took 14 us; one 1024-thread workgroup per row, 7.7 us under the
+// kernel tracer.  The quarter split takes a B = 1, 8/4, 128K-key forward
+// from 44.2 to 42.0 us.)
+#ifndef GFA_FC_DS
+#define GFA_FC_DS 4
+#endif
+constexpr int FC_THREADS = 1024, FC_DS = GFA_FC_DS, FC_DCH = 32 / FC_DS, FC_GROUPS = FC_THREADS / FC_DCH, FC_U = 8;
 __global__ __launch_bounds__(FC_THREADS) void flat_combine_kernel(FlatParams p) {
     __shared__ float sm_m[FC_GROUPS], sm_l[FC_GROUPS];
-    __shared__ float4_t sm_o[FC_GROUPS][32];
+    __shared__ float4_t sm_o[FC_GROUPS][FC_DCH];
     const int seg = blockIdx.x, r = blockIdx.y;
     const int nrows = p.Sq * p.G;
-    const int t = threadIdx.x, grp = t >> 5, d0 = 4 * (t & 31);
+    const int t = threadIdx.x, grp = t / FC_DCH, dc = t % FC_DCH, d0 = 4 * (blockIdx.z * FC_DCH + dc);
     float M = -INFINITY, L = 0.f;
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
     const float *base = p.ws + ((int64_t)seg * p.P * nrows + r) * FD_ROW;
@@ -2615,29 +2621,33 @@ __global__ __launch_bounds__(FC_THREADS) void flat_combine_kernel(FlatParams p) 
             }
         }
     }
-    if ((t & 31) == 0) {
-        sm_m[grp] = M;
-        sm_l[grp] = L;
+    // tree merge of the groups' states through LDS
+#pragma unroll
+    for (int half = FC_GROUPS / 2; half >= 1; half >>= 1) {
+        if (grp >= half && grp < 2 * half) {
+            if (dc == 0) {
+                sm_m[grp] = M;
+                sm_l[grp] = L;
+            }
+            sm_o[grp][dc] = acc;
+        }
+        __syncthreads();
+        if (grp < half) {
+            const float m2 = sm_m[grp + half];
+            const float mn = fmaxf(M, m2);
+            const float a = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+            const float b = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
+            L = fmaf(L, a, sm_l[grp + half] * b);
+            acc = acc * a + sm_o[grp + half][dc] * b;
+            M = mn;
+        }
+        __syncthreads();
     }
-    sm_o[grp][t & 31] = acc;
-    __syncthreads();
     if (grp != 0) return;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < FC_GROUPS; ++k) mx = fmaxf(mx, sm_m[k]);
-    const float ms = mx == -INFINITY ? 0.0f : mx;
-    float l = 0.f;
-    float4_t o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < FC_GROUPS; ++k) {
-        const float wk = sm_m[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm_m[k] - ms);
-        l = fmaf(sm_l[k], wk, l);
-        o += sm_o[k][t & 31] * wk;
-    }
     const int b = seg / p.Hkv, h = seg - b * p.Hkv;
     const int j = r / p.G, hq = h * p.G + (r - j * p.G);
-    const float inv = l > 0.f ? 1.0f / l : 0.0f;
-    *reinterpret_cast<float4_t *>(p.out + (int64_t)(b * p.Sq + j) * p.o_ts + (int64_t)hq * p.o_hs + d0) = o * inv;
+    const float inv = L > 0.f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<float4_t *>(p.out + (int64_t)(b * p.Sq + j) * p.o_ts + (int64_t)hq * p.o_hs + d0) = acc * inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -3364,7 +3374,7 @@ extern "C" hipError_t gfx906_fa_amd_flat_decode(
         case GFA_DTYPE_F16: flat_decode_kernel<GFA_DTYPE_F16><<<(unsigned)grid, 64, 0, stream>>>(p); break;
         default: flat_decode_kernel<GFA_DTYPE_BF16><<<(unsigned)grid, 64, 0, stream>>>(p); break;
     }
-    if (P > 1) flat_combine_kernel<<<dim3(nseg, seq_q * G), FC_THREADS, 0, stream>>>(p);
+    if (P > 1) flat_combine_kernel<<<dim3(nseg, seq_q * G, FC_DS), FC_THREADS, 0, stream>>>(p);
     return hipGetLastError();
 }
 
