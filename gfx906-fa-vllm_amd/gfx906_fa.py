@@ -476,8 +476,11 @@ def paged_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: t
         _cuda(t, n)
     _check(query.dtype in _DT, "query must be fp16, bf16 or fp32")
     _check(query.dim() == 3 and query.shape[2] == 128, "query must be [num_tokens, Hq, 128]")
-    _check(query.stride(2) == 1, "query rows must be contiguous")
     T, Hq, D = query.shape
+    if T == 0:  # no query rows: nothing to compute or write (an empty tensor's strides are arbitrary)
+        return out if out is not None else torch.empty((0, Hq, D), dtype=out_dtype or query.dtype,
+                                                       device=query.device)
+    _check(query.stride(2) == 1, "query rows must be contiguous")
     bs, Hkv, cbs, chs = _plane_info(key_cache, value_cache)
     _check(Hq % Hkv == 0, f"heads_q={Hq} must be divisible by heads_kv={Hkv}")
     _check(block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1,

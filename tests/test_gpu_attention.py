@@ -209,6 +209,22 @@ def test_empty_sequences():
     assert_close(o, ref)
 
 
+def test_zero_token_batch():
+    """Every sequence with an empty query (num_tokens 0, whatever strides the
+    empty query tensor has): an empty output and no launch."""
+    need_gpu()
+    announce("zero-token batch")
+    b = W.build_batch([1467, 30], [0, 0], 12, 2, seed=12)
+    assert b.num_tokens == 0
+    out = W.attention(b, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (0, 12, 128)
+    q = torch.empty((0, 12, 128), dtype=torch.float16, device=DEV).as_strided((0, 12, 128), (0, 0, 0))
+    kp, vp = b.planes()
+    out = gfx906_fa.paged_attention(q, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t, 0, b.max_seq_len, b.scale)
+    assert out.numel() == 0
+
+
 def test_forward_paged_direct_padded():
     """Reference-signature padded entry: non-causal (kv_max cutoff) and
     inline-causal via q_abs_offset (extension/gfx906_fa.cpp:516-658)."""
