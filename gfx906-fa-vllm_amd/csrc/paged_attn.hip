@@ -1632,10 +1632,6 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     float16v_t sacc[PF_NST];  // S' of the tile between its two half-steps
     // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile (stage kst)
     auto qk = [&](const uint8_t *kst) __attribute__((always_inline)) {
-        // scheduling hint for this block (LLVM's small-GEMM interleave: each
-        // K^ operand read issued right behind the MFMA before it).  Same
-        // registers; cfg3 11.48 -> 11.31 ms and cfg4 5.93 -> 5.85 ms on one box.
-        __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
             {   // -m in all 16 accumulator registers, built as a 64-bit splat
@@ -1653,6 +1649,18 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
                 sacc[st] = mfma32(a, qf[kk], sacc[st]);
             }
         }
+        // Schedule of this block: the K^ operand reads run two ahead of the
+        // MFMAs (read, read, then MFMA / read pairs), in the registers of
+        // the two in flight.  The compiler's own order waited for each pair
+        // before its two MFMAs.  One box: cfg3 11.48 -> 11.20 ms, cfg4 5.93
+        // -> 5.83 ms; three ahead: cfg3 11.22 ms, cfg4 5.90 ms.
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS reads
+#pragma unroll
+        for (int i = 0; i < 8 * PF_NST - 1; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     };
     // softmax and O += P V^ over tile kt (stage vst)
     auto sv = [&](int kt, const uint8_t *vst) __attribute__((always_inline)) {
