@@ -227,10 +227,15 @@ __device__ __forceinline__ void acc_init(WaveAcc<NRG> &a) {
 // (d_v <= 65504/127) and for bf16 V with |v| < 1.3e5.
 constexpr float LAZY_TAU = 6.0f;
 
-// Max of three through fmaxf (the compiler forms v_max3_f32).  Not inline
-// assembly: the compiler's wait states between an MFMA and a VALU read of
-// its result do not cover instructions inside asm statements.
-__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+// Max of three as the IEEE 754-2019 maximum (NaN-propagating): the compiler
+// forms v_maximum3_f32 and, unlike fmaxf on MFMA results, needs no
+// canonicalizing v_max_f32 x, x first (a 32-value tree: 16 instructions,
+// against 18).  Not inline assembly: the compiler's wait states between an
+// MFMA and a VALU read of its result do not cover instructions inside asm
+// statements.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 
 __device__ __forceinline__ float4_t mfma16k16(half4_t a, half4_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -1632,17 +1637,26 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_prefill_kernel(AttnParams p
     float16v_t sacc[PF_NST];  // S' of the tile between its two half-steps
     // S'^T = K^ . Q^T - m for the 32-key subtiles of the tile (stage kst)
     auto qk = [&](const uint8_t *kst) __attribute__((always_inline)) {
+        // -m in all 16 accumulator registers, the srcC of the first MFMA of
+        // both chains.  Each 64-bit pair passes through an empty asm so that
+        // the compiler copies it with one v_mov_b64 (7 moves, against 15
+        // v_mov_b32 for a plain splat).  Empty asm statements count as no
+        // wait states, so the VALU-write -> MFMA-read gap is still enforced.
+        float16v_t msp;
+        {
+            const uint64_t pr = ((uint64_t)__float_as_uint(-m_use) << 32) | __float_as_uint(-m_use);
+            u64x8_t sp;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint64_t t = pr;
+                asm volatile("" : "+v"(t));
+                sp[e] = t;
+            }
+            msp = __builtin_bit_cast(float16v_t, sp);
+        }
 #pragma unroll
         for (int st = 0; st < PF_NST; ++st) {
-            {   // -m in all 16 accumulator registers, built as a 64-bit splat
-                // (the compiler then builds it once per tile and feeds it to
-                // the first MFMA of both chains as srcC)
-                const uint64_t pr = ((uint64_t)__float_as_uint(-m_use) << 32) | __float_as_uint(-m_use);
-                u64x8_t sp;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sp[e] = pr;
-                sacc[st] = __builtin_bit_cast(float16v_t, sp);
-            }
+            sacc[st] = msp;
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
                 const half8_t a = *reinterpret_cast<const half8_t *>(kst + kread + 32 * st * PF_KPITCH + 32 * kk);
