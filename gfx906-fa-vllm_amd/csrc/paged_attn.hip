@@ -690,9 +690,20 @@ __device__ __forceinline__ int range_of(int64_t U, int64_t u, int n) { return (i
 // CHUNK: sequences may have more rows than one tile (up to dec_rows_max):
 // each piece is streamed once per R-row chunk.  A separate instantiation, so
 // the launches that never need it keep their register allocation.
+// Waves per decode workgroup.  The 32-row class in one row chunk (verify
+// tiles) runs one 8-wave workgroup per CU (137 KB of LDS: eight ring slices)
+// instead of two 4-wave ones: half the pieces, and one cross-wave merge per
+// CU.  Measured on three boxes: 6/1, 8 x (131072 + 5) 1.4-4 % faster, 48/8
+// within -0.8..+0.5 %.  The 16- and 48-row classes measured slower that way
+// (the fused cache write of a decode step; 14 spilled VGPRs), and the
+// two-chunk mode pairs its waves two by two.
+constexpr int dec_nw(int nrg, bool chunk) { return nrg == 2 && !chunk ? 8 : DEC_NW; }
+
 template <int NRG, int QDT, int ODT, bool CHUNK = false>
-__global__ __launch_bounds__(64 * DEC_NW)
+__global__ __launch_bounds__(64 * dec_nw(NRG, CHUNK))
 __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void attn_decode_kernel(AttnParams p) {
+    constexpr int NW = dec_nw(NRG, CHUNK);  // waves in this workgroup
+    static_assert((NW & (NW - 1)) == 0, "sub-pages are dealt to the waves by js & (NW - 1)");
     constexpr int R = 16 * NRG;  // rows per slot
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -780,7 +791,7 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         // below over this workgroup's pieces.  The step's new tokens (positions
         // sl - n_q .. sl - 1, input rows q0 ..) that lie in a piece's
         // sub-pages are quantized and stored by the wave that will stream
-        // their sub-page (wave (js - a) % DEC_NW takes sub-page js of piece
+        // their sub-page (wave (js - a) % NW takes sub-page js of piece
         // [a, b)), so each new (token, kv-head) is written by the wave that
         // reads it in this launch (by both, in the two-chunk mode), and that
         // wave's later loads follow its own stores in program order.
@@ -798,7 +809,7 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
             // write its new tokens (the same bytes), each before its own loads
             const bool dual = CHUNK && sv.nq * p.G > R;
             for (int js = max(a, lo >> 4); js < b; ++js) {  // uniform
-                if (dual ? (((js - a) & 1) != (wv & 1)) : (((js - a) & (DEC_NW - 1)) != wv)) continue;
+                if (dual ? (((js - a) & 1) != (wv & 1)) : (((js - a) & (NW - 1)) != wv)) continue;
                 const int t_hi = min(16 * js + 16, sv.sl);
                 for (int pos = max(16 * js, lo); pos < t_hi; ++pos)
                     write_new_token<QDT>(p, hh, sv.q0 + (pos - lo), lane);
@@ -823,8 +834,8 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
     // passes), or (verify tiles) its LDS ring while it streams; rows past R
     // only lengthen the slice for the ring
     constexpr int RA = NRG >= 2 ? cmax(R < 32 ? R : 32, (DEC_RING * DEC_RING_SLOT + 4 * 132 - 1) / (4 * 132)) : R;
-    __shared__ float sm_o[DEC_NW][RA][128 + 4];
-    __shared__ float sm_m[DEC_NW][R], sm_l[DEC_NW][R];
+    __shared__ float sm_o[NW][RA][128 + 4];
+    __shared__ float sm_m[NW][R], sm_l[NW][R];
     int64_t u = u0;
     bool first = true;
     while (u < u1) {
@@ -883,7 +894,7 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         }
         __syncthreads();
         const int r_hi = NPASS == 1 ? rows_c : min(rows_c, 32 * ps + 32);
-        for (int it = threadIdx.x + 32 * 32 * ps; it < r_hi * 32; it += 64 * DEC_NW) {
+        for (int it = threadIdx.x + 32 * 32 * ps; it < r_hi * 32; it += 64 * NW) {
             const int r = it >> 5, d0 = (it & 31) * 4;
             const int ch = CHUNK ? r / R : 0;   // the row's chunk: waves ch*wpc .. ch*wpc + wpc - 1
             const int rl = r - ch * R;          // its row inside the chunk
@@ -918,11 +929,11 @@ __attribute__((amdgpu_waves_per_eu(DecCfg<NRG>::wpe, DecCfg<NRG>::wpe))) void at
         __syncthreads();  // LDS reused by the next pass or piece
         }
         };
-        static_assert(DEC_NW == 4 && DEC_CHUNK_ROWS <= 2 * 32, "two row chunks of two waves each");
+        static_assert((NW == 4 || !CHUNK) && DEC_CHUNK_ROWS <= 2 * 32, "two row chunks of two waves each");
         if (CHUNK && nrows > R) {  // uniform: rows R..nrows-1 (nrows <= 2R) in the second chunk
-            rows_pass(R * (wv >> 1), wv & 1, 2, DEC_NW / 2);
+            rows_pass(R * (wv >> 1), wv & 1, 2, NW / 2);
         } else {
-            rows_pass(0, wv, DEC_NW, DEC_NW);
+            rows_pass(0, wv, NW, NW);
         }
         u += b - a;
         first = false;
@@ -2955,7 +2966,11 @@ hipError_t launch_all(const AttnParams &p0, const Plan &pl, char *ws, int num_se
             attn_combine_kernel<3, ODT><<<dim3(num_seqs, num_kv_heads, crow), 256, 0, stream>>>(pd);
         } else {
             if (c.rows_hi > 32) attn_decode_kernel<2, QDT, ODT, true><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
-            else attn_decode_kernel<2, QDT, ODT><<<c.nwg, 64 * DEC_NW, 0, stream>>>(pd);
+            else {  // one 8-wave workgroup where the plan sized two 4-wave ones
+                constexpr int nw = dec_nw(2, false);
+                pd.nwg = c.nwg * DEC_NW / nw;
+                attn_decode_kernel<2, QDT, ODT><<<pd.nwg, 64 * nw, 0, stream>>>(pd);
+            }
             if (c.rows_lo > 0 && (int64_t)num_seqs * num_kv_heads >= GFA_COMB_SEGS)
                 attn_combine_few_kernel<ODT><<<dim3(num_seqs, num_kv_heads), 256, 0, stream>>>(pd);
             else

@@ -524,6 +524,27 @@ def test_decode_short_contexts_split(case):
     assert_close(to_np_f32(out), batch_oracle(b))
 
 
+def test_verify_tiles_one_workgroup_per_cu():
+    """5-token verify steps at 6/1 (30 rows per kv-head: the 32-row class in
+    one row chunk) run one 8-wave workgroup per CU: a batch long enough to
+    fill the device publishes exactly as many decode workgroups as the device
+    has CUs (header word 1 of the decode workspace), its segments are split
+    over them, and the output matches the oracle."""
+    need_gpu()
+    announce("verify tiles, one workgroup per CU: 8 x (16384 + 5), 6/1")
+    b = W.build_batch([16384 + 5] * 8, [5] * 8, 6, 1, seed=77)
+    kp, vp = b.planes()
+    ws = gfx906_fa.new_workspace(gfx906_fa.workspace_size(b.num_seqs, b.num_tokens, b.Hq, b.Hkv, b.max_query_len,
+                                                          b.max_seq_len), b.device)
+    out = gfx906_fa.paged_attention(b.query, kp, vp, b.block_table, b.seq_lens_t, b.qsl_t, b.max_query_len,
+                                    b.max_seq_len, b.scale, workspace=ws, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    u, nwg = ws[:16].view(torch.int64).cpu().tolist()
+    cus = torch.cuda.get_device_properties(b.device).multi_processor_count
+    assert u == 8 * ((16384 + 5 + 15) // 16) and nwg == cus, (u, nwg, cus)
+    assert_close(to_np_f32(out), batch_oracle(b))
+
+
 @pytest.mark.parametrize("nseq", [63, 64, 65])
 def test_decode_batch_size_boundary(nseq):
     """Batches on both sides of 64 sequences (the decode kernel locates its
