@@ -236,6 +236,11 @@ constexpr float LAZY_TAU = 6.0f;
 __device__ __forceinline__ float max3f(float a, float b, float c) {
     return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
+// Max of a lane's four scores the same way: v_maximum + v_maximum3 (fmaxf
+// needs two canonicalizing moves and two maxes).
+__device__ __forceinline__ float max4f(const float (&v)[4]) {
+    return max3f(v[0], v[1], __builtin_elementwise_maximum(v[2], v[3]));
+}
 
 __device__ __forceinline__ float4_t mfma16k16(half4_t a, half4_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -278,7 +283,7 @@ __device__ __forceinline__ void attend_subpage(WaveAcc<NRG> &acc, const SubPage 
         // The lane's max over its 4 keys; a row's max is the largest of its
         // four lanes' (i16 + 16 g), so no lane above m + LAZY_TAU means no row
         // is, and the cross-lane step runs only when some row may rescale.
-        const float ml = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])) * c;
+        const float ml = max4f(sv) * c;
         if (__builtin_amdgcn_ballot_w64(ml > acc.m[rg] + LAZY_TAU)) {  // wave-uniform, rare after warm-up
             const float mt = xrow_max(ml);
             const bool need = mt > acc.m[rg] + LAZY_TAU;
@@ -2554,7 +2559,7 @@ __global__ __launch_bounds__(64) void flat_decode_kernel(FlatParams p) {
         }
         // lane-local test first; the row's max (over lanes i16 + 16 g) only
         // when some lane may rescale
-        const float ml = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])) * c;
+        const float ml = max4f(sv) * c;
         if (__builtin_amdgcn_ballot_w64(ml > m + LAZY_TAU)) {  // wave-uniform, rare after warm-up
             const float mt = xrow_max(ml);
             const bool need = mt > m + LAZY_TAU;
