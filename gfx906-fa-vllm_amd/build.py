@@ -27,7 +27,8 @@ def hipcc() -> str:
 
 def build(verbose: bool = False, out: str | None = None, defines=()) -> str:
     """Compiles csrc/*.hip into `out` (default: the in-tree library).
-    `defines`: extra -D tuning macros (GFA_DEC_DEPTH, GFA_DEC_NW, GFA_SPLIT_WGS)."""
+    `defines`: extra -D tuning macros (GFA_DEC_DEPTH, GFA_DEC_RING, GFA_PF_PDEPTH, ...: the
+    `#ifndef GFA_*` defaults in csrc/)."""
     out = out or os.path.join(HERE, LIB_NAME)
     tmp = out + ".tmp"
     cmd = [
